@@ -1,0 +1,295 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 PQ2_0 matmul path (one MI355X).
+
+Headline (BASELINE.json metric): decode GEMV GB/s at 17408x5120 (config 1's
+gate/up shape), batch 1.  A "step" is one bonsai_p40_gemv over one
+17408x5120 PQ2_0 matrix with an already-quantised activation resident in HBM.
+The weights rotate through enough distinct copies (>= 1.1 GB) that every step
+streams its matrix from HBM rather than from the 256 MB Infinity Cache.
+
+`value` = algorithmic bytes per GEMV (W + Q8_1 activation + fp32 output =
+23,750,272 B) / measured time per GEMV.  Timing uses HIP events on the stream
+the kernels run on (torch's current stream, whose handle is passed to the C
+ABI).  The same JSON line carries the roofline of that kernel, secondary
+measurements (configs 0-4: FWHT+Q8_1 pre-pass, FFN chain, per-token sweep,
+small batch, prefill GEMM TOPS) and the CPU baseline: the reference's own host
+GEMV (compiled from the reference sources into oracle/_ref) timed on this
+host's cores on a bounded sample of the same workload.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "p40-kernel_amd"))
+
+import torch  # noqa: E402
+
+import bonsai_p40 as B  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA
+N_EMBD, N_FF, Q_DIM, KV_DIM, N_LAYER = 5120, 17408, 6144, 1024, 64
+
+
+def gemv_bytes(n_out: int, n_in: int, n_tok: int = 1) -> int:
+    return B.pq2_bytes(n_out, n_in) + n_tok * (B.q8_bytes(n_in) + 4 * n_out)
+
+
+# ------------------------------------------------------ synthetic inputs
+def synth_weights(n_out: int, n_in: int, gen: torch.Generator) -> torch.Tensor:
+    """PQ2_0 blocks on the GPU: codes {0,1,2} w.p. (1-0.001)/3 each, code 3
+    w.p. 0.001; d = fp16(|N(0, 0.02)| + 1e-4)."""
+    nb = n_in // B.QK_PQ2
+    nblk = n_out * nb
+    u = torch.rand((nblk, 32, 4), generator=gen, device="cuda")
+    codes = torch.where(u <= 0.001, torch.full_like(u, 3.0),
+                        torch.clamp(torch.floor((u - 0.001) / (0.999 / 3)), max=2.0)).to(torch.int32)
+    packed = (codes[..., 0] | (codes[..., 1] << 2) | (codes[..., 2] << 4) | (codes[..., 3] << 6)).to(torch.uint8)
+    d = (torch.randn((nblk,), generator=gen, device="cuda").abs() * 0.02 + 1e-4).to(torch.float16)
+    blocks = torch.empty((nblk, B.PQ2_BYTES), dtype=torch.uint8, device="cuda")
+    blocks[:, 0:2] = d.view(torch.uint8).view(nblk, 2)
+    blocks[:, 2:] = packed
+    return blocks.view(-1)
+
+
+def synth_activation_q8(n_in: int, gen: torch.Generator, n_tok: int = 1) -> torch.Tensor:
+    """N(0,1) token rows -> FWHT-1024 -> Q8_1, through the product pre-pass."""
+    x = torch.randn((n_tok, n_in), generator=gen, device="cuda")
+    q = torch.empty(B.q8_bytes(n_in, n_tok), dtype=torch.uint8, device="cuda")
+    if n_tok == 1:
+        B.fwht_quant(x, None, q, n_in)
+    else:
+        B.quant_tokens(x, None, q, n_in, n_tok, True)
+    return q
+
+
+# --------------------------------------------------------------- timing
+def time_loop(fn, steps: int, warmup: int) -> float:
+    """ms per call of fn(i), HIP events on the current stream."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        fn(warmup + i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def copies_for(nbytes: int, target: float = 1.1e9) -> int:
+    return max(2, math.ceil(target / nbytes))
+
+
+def bench_gemv(n_out, n_in, steps, warmup, gen, n_tok=1):
+    W0 = synth_weights(n_out, n_in, gen)
+    R = copies_for(W0.numel())
+    Ws = [W0] + [W0.clone() for _ in range(R - 1)]
+    xq = synth_activation_q8(n_in, gen, n_tok)
+    y = torch.empty(n_out * n_tok, dtype=torch.float32, device="cuda")
+    if n_tok == 1:
+        fn = lambda i: B.gemv(Ws[i % R], xq, y, n_out, n_in)  # noqa: E731
+    else:
+        fn = lambda i: B.gemm(Ws[i % R], xq, y, n_out, n_in, n_tok)  # noqa: E731
+    ms = time_loop(fn, steps, warmup)
+    del Ws
+    return ms
+
+
+def bench_prepass(n, steps, warmup, gen):
+    x = torch.randn(n, generator=gen, device="cuda")
+    q = torch.empty(B.q8_bytes(n), dtype=torch.uint8, device="cuda")
+    return time_loop(lambda i: B.fwht_quant(x, None, q, n), steps, warmup)
+
+
+def bench_ffn_chain(steps, warmup, gen):
+    """Config 1: pre-pass, gate + up GEMVs, SwiGLU+FWHT+Q8_1, down GEMV."""
+    sets = []
+    per = 3 * B.pq2_bytes(N_FF, N_EMBD)
+    R = copies_for(per)
+    base = [synth_weights(N_FF, N_EMBD, gen), synth_weights(N_FF, N_EMBD, gen),
+            synth_weights(N_EMBD, N_FF, gen)]
+    for r in range(R):
+        sets.append(base if r == 0 else [w.clone() for w in base])
+    x = torch.randn(N_EMBD, generator=gen, device="cuda")
+    xq = torch.empty(B.q8_bytes(N_EMBD), dtype=torch.uint8, device="cuda")
+    hq = torch.empty(B.q8_bytes(N_FF), dtype=torch.uint8, device="cuda")
+    g = torch.empty(N_FF, device="cuda")
+    u = torch.empty(N_FF, device="cuda")
+    y = torch.empty(N_EMBD, device="cuda")
+
+    def step(i):
+        Wg, Wu, Wd = sets[i % R]
+        B.fwht_quant(x, None, xq, N_EMBD)
+        B.gemv(Wg, xq, g, N_FF, N_EMBD)
+        B.gemv(Wu, xq, u, N_FF, N_EMBD)
+        B.swiglu_fwht_quant(g, u, None, hq, N_FF)
+        B.gemv(Wd, hq, y, N_EMBD, N_FF)
+
+    ms = time_loop(step, steps, warmup)
+    del sets, base
+    return ms, per + 0  # weight bytes per chain
+
+
+def bench_token_sweep(steps, warmup, gen):
+    """Config 2: 64 layers x (q, k, v, o, gate, up, down), each GEMV with its
+    own FWHT+Q8_1 pre-pass; 5.79 GB of distinct weights per token."""
+    shapes = [(Q_DIM, N_EMBD), (KV_DIM, N_EMBD), (KV_DIM, N_EMBD), (N_EMBD, Q_DIM),
+              (N_FF, N_EMBD), (N_FF, N_EMBD), (N_EMBD, N_FF)]
+    proto = {s: synth_weights(s[0], s[1], gen) for s in set(shapes)}
+    layers = [[proto[s].clone() for s in shapes] for _ in range(N_LAYER)]
+    xs = {n: torch.randn(n, generator=gen, device="cuda") for n in (N_EMBD, Q_DIM, N_FF)}
+    qs = {n: torch.empty(B.q8_bytes(n), dtype=torch.uint8, device="cuda") for n in xs}
+    ys = {n: torch.empty(n, device="cuda") for n in (Q_DIM, KV_DIM, N_EMBD, N_FF)}
+    wbytes = sum(B.pq2_bytes(*s) for s in shapes) * N_LAYER
+
+    def token(i):
+        for L in layers:
+            for (n_out, n_in), W in zip(shapes, L):
+                B.fwht_quant(xs[n_in], None, qs[n_in], n_in)
+                B.gemv(W, qs[n_in], ys[n_out], n_out, n_in)
+
+    ms = time_loop(token, steps, warmup)
+    del layers, proto
+    return ms, wbytes
+
+
+def cpu_baseline(sample_s: float):
+    """The reference host GEMV (oracle/_ref = reference sources compiled here;
+    the restatement oracle/liboracle.so if _ref is absent), 1 thread, on
+    17408x5120 matrices of the same distribution, for about sample_s seconds."""
+    sys.path.insert(0, ROOT)
+    import numpy as np
+    from oracle import oracle as O
+    R = O.ref()
+    n_out, n_in = N_FF, N_EMBD
+    W = O.gen_weights(77, n_out, n_in)
+    xq = O.quantize_q8_1(O.fwht(O.gen_normal(78, n_in)), True)
+    y = np.empty(n_out, np.float32)
+    if R is not None:
+        kind = "reference"
+        fn = lambda: R.ref_gemv(O._p(W, O._u8p), O._p(xq, O._u8p), O._p(y, O._f32p), n_out, n_in)  # noqa: E731
+    else:
+        kind = "port"
+        fn = lambda: O.lib().orc_gemv(O._p(W, O._u8p), O._p(xq, O._u8p), O._p(y, O._f32p), n_out, n_in, 1)  # noqa: E731
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        fn()
+        n += 1
+        if time.perf_counter() - t0 >= sample_s:
+            break
+    dt = (time.perf_counter() - t0) / n
+    return {"value": round(gemv_bytes(n_out, n_in) / dt / 1e9, 4), "unit": "GB/s", "cores": 1,
+            "kind": kind, "ms_per_gemv": round(dt * 1e3, 3),
+            "sample": f"{n} single-thread host GEMVs of 17408x5120 (pq2_0_row_dot_perm per row), "
+                      f"{n * dt:.1f} s"}
+
+
+def load_traffic(path):
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--quick", action="store_true", help="headline only (no secondary configs)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--only-gemv", action="store_true", help="headline GEMV loop only (profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the PQ2_0 path would shard by rows; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    B.lib()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1234)
+
+    # ---- headline: decode GEMV 17408x5120
+    ms = bench_gemv(N_FF, N_EMBD, args.steps, args.warmup, gen)
+    nbytes = gemv_bytes(N_FF, N_EMBD)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    print(f"[bench] gemv 17408x5120: {ms * 1e3:.2f} us  {gbs:.1f} GB/s", file=sys.stderr, flush=True)
+    if args.only_gemv:
+        return
+
+    extra = {}
+    if not args.quick:
+        for (n_out, n_in, tag) in ((N_EMBD, N_FF, "gemv_5120x17408"), (N_EMBD, N_EMBD, "gemv_5120x5120")):
+            m = bench_gemv(n_out, n_in, args.steps, args.warmup, gen)
+            extra[tag] = {"us": round(m * 1e3, 3), "GB/s": round(gemv_bytes(n_out, n_in) / (m * 1e-3) / 1e9, 1)}
+            print(f"[bench] {tag}: {extra[tag]}", file=sys.stderr, flush=True)
+        for n in (N_EMBD, N_FF):
+            m = bench_prepass(n, args.steps, args.warmup, gen)
+            extra[f"fwht_quant_{n}_us"] = round(m * 1e3, 3)
+        m, wb = bench_ffn_chain(max(20, args.steps // 4), 5, gen)
+        extra["ffn_chain_config1"] = {"us": round(m * 1e3, 2), "weight_GB/s": round(wb / (m * 1e-3) / 1e9, 1)}
+        print(f"[bench] ffn chain: {extra['ffn_chain_config1']}", file=sys.stderr, flush=True)
+        m, wb = bench_token_sweep(5, 2, gen)
+        extra["token_sweep_config2"] = {"ms_per_token": round(m, 3), "tok/s": round(1e3 / m, 2),
+                                        "weight_GB/s": round(wb / (m * 1e-3) / 1e9, 1),
+                                        "weight_bytes": wb}
+        print(f"[bench] token sweep: {extra['token_sweep_config2']}", file=sys.stderr, flush=True)
+        for bt in (2, 4, 8):
+            for (n_out, n_in) in ((N_FF, N_EMBD), (N_EMBD, N_FF)):
+                m = bench_gemv(n_out, n_in, max(20, args.steps // 2), 10, gen, n_tok=bt)
+                extra[f"small_batch_B{bt}_{n_out}x{n_in}"] = {
+                    "us": round(m * 1e3, 2), "GB/s": round(gemv_bytes(n_out, n_in, bt) / (m * 1e-3) / 1e9, 1)}
+        print(f"[bench] small batch done", file=sys.stderr, flush=True)
+        for M in (512, 2048):
+            for (n_out, n_in) in ((N_FF, N_EMBD), (N_EMBD, N_FF)):
+                m = bench_gemv(n_out, n_in, 10, 3, gen, n_tok=M)
+                tops = 2.0 * M * n_out * n_in / (m * 1e-3) / 1e12
+                extra[f"prefill_M{M}_{n_out}x{n_in}"] = {"us": round(m * 1e3, 1), "TOPS": round(tops, 1),
+                                                         "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+                print(f"[bench] prefill M={M} {n_out}x{n_in}: {extra[f'prefill_M{M}_{n_out}x{n_in}']}",
+                      file=sys.stderr, flush=True)
+
+    traffic = load_traffic(os.path.join(ROOT, "profiles", "gemv_17408x5120_traffic.json"))
+    roof = {"bound": "hbm", "kernel": "gemv_stream_kernel (bonsai_p40_gemv)",
+            "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic.get("bytes_per_launch") if traffic else None,
+            "algorithmic_bytes": nbytes}
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(args.cpu_seconds)
+        print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+
+    line = {
+        "metric": "PQ2_0 decode GEMV GB/s (% HBM peak) at 17408x5120; prefill GEMM int8 TOPS",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded PQ2_0 codes/scales of config 0 distribution; N(0,1) -> FWHT -> Q8_1)",
+        "config": {"workload": "decode GEMV 17408x5120 PQ2_0 x Q8_1 (config 1 gate/up), batch 1, "
+                               f"weights rotated over {copies_for(B.pq2_bytes(N_FF, N_EMBD))} HBM copies",
+                   "n_out": N_FF, "n_in": N_EMBD, "bytes_per_step": nbytes},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,128 @@
+// bonsai_p40.h -- C ABI of the MI355X (gfx950) PQ2_0 matmul path.
+//
+// Drop-in for the reference header include/bonsai_p40.h of
+// boetti-dev/p40-kernel: every declaration of that header is kept with the
+// same name, argument order, argument meaning and return-code convention, so
+// C++ host code written against it links against libbonsai_p40.so unchanged.
+// The library is written for AMD CDNA4 (gfx950) in HIP; `bonsai_stream` is a
+// hipStream_t (NULL = the default stream).
+//
+// Conventions shared by every entry point (reference: gemv_p40.cu:200-219,
+// gemm_p40.cu:143-154, gemv_repack_p40.cu:196-220, elementwise_p40.cu:75-80):
+//   * all pointers are device pointers owned by the caller; nothing is
+//     allocated and nothing synchronises -- work is enqueued on `stream`;
+//   * return 1 for invalid arguments, 0 for an empty no-op, otherwise the
+//     hipError_t of the launch (so 0 = enqueued).  Callers test `!= 0`;
+//   * block_pq2_0 = 34 bytes (fp16 d, 32 bytes of 2-bit codes, element j in
+//     byte j/4 at bits 2(j%4), value (code-1)*d); block_q8_1 = 36 bytes (fp16
+//     d, int16 sum s stored as raw bits, 32 int8 in the PQ2_0-native permuted
+//     order: position j holds element 16(j>>4) + 4(j&3) + ((j>>2)&3));
+//   * Q8_1 buffers must be 4-byte aligned.  PQ2_0 weights need only the
+//     2-byte alignment of the format; 16-byte aligned weights with
+//     n_in % 1024 == 0 take the streaming fast path.
+//   * rounding follows the reference HOST code (src/pq2_0.h:99-126,
+//     src/p40_common.h:82-114): q = lroundf(x/d) (ties away from zero) and the
+//     fp16 scale rounds ties away from zero, so Q8_1 bytes equal the host's.
+#pragma once
+
+#include <cstdint>
+#include <cstddef>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// Opaque stream handle (a hipStream_t), reference include/bonsai_p40.h:16.
+typedef void * bonsai_stream;
+
+// --- decode (batch = 1) matrix-vector -------------------------------------
+// y[n_out] = W[n_out, n_in] . x with x already in permuted Q8_1 (xq).
+// Replaces include/bonsai_p40.h:21-22 (src/kernels/gemv_p40.cu:210-219).
+// Errors: 1 if n_in <= 0 or n_in % 128 != 0 or xq is not 4-byte aligned;
+// 0 (no-op) if n_out <= 0.
+int bonsai_p40_gemv(const void * W, const void * xq, float * y,
+                    int64_t n_out, int64_t n_in, bonsai_stream stream);
+
+// Quantise n floats to permuted Q8_1 (n/32 blocks of 36 bytes).
+// Replaces include/bonsai_p40.h:25 (src/kernels/gemv_p40.cu:200-208).
+// Errors: 1 if n <= 0 or n % 32 != 0.
+int bonsai_p40_quant_activations(const float * x, void * out, int64_t n, bonsai_stream stream);
+
+// --- prefill (batch > 1) ----------------------------------------------------
+// Y[n_out, n_tok] (row-major, Y[r*n_tok + t]) = W . X, X in permuted Q8_1,
+// chunk-major: block (c, t) at index c*n_tok + t (src/kernels/gemm_p40.cu:75).
+// Replaces include/bonsai_p40.h:29-30 (src/kernels/gemm_p40.cu:143-154).
+// n_tok <= 8 runs the bandwidth-bound small-batch kernel, larger n_tok the
+// int8-MFMA tile GEMM.  Errors: 1 if n_in <= 0 or n_in % 128 != 0;
+// 0 (no-op) if n_out <= 0 or n_tok <= 0.
+int bonsai_p40_gemm(const void * W, const void * Xq, float * Y,
+                    int64_t n_out, int64_t n_in, int64_t n_tok, bonsai_stream stream);
+
+// --- aligned repacked layout ------------------------------------------------
+// Size-neutral row: d[nb] fp16, then 4 planes of nb 8-byte code units; unit
+// u = plane*nb + block at byte 2*nb + 8u (src/pq2_0_repack.h:46-57).
+// src and dst must not overlap.  Errors: 1 if n_in % 128 != 0, n_out <= 0 or
+// n_in/128 is not a positive multiple of 8.
+// Replaces include/bonsai_p40.h:35 (src/kernels/gemv_repack_p40.cu:196-207).
+int bonsai_p40_repack(const void * src, void * dst, int64_t n_out, int64_t n_in, bonsai_stream stream);
+// y = W_repacked . x for fp32 x (quantised to Q8_1 inside the kernel).
+// Replaces include/bonsai_p40.h:36-37 (src/kernels/gemv_repack_p40.cu:209-220).
+// Errors: as bonsai_p40_repack, plus 1 if the quantised activation
+// (n_in/32 * 40 bytes) does not fit the 160 KiB LDS of a workgroup.
+int bonsai_p40_gemv_repack(const void * W, const float * x, float * y,
+                           int64_t n_out, int64_t n_in, bonsai_stream stream);
+
+// --- transforms -----------------------------------------------------------------
+// In-place normalised Sylvester-Hadamard transform in blocks of 1024, signs
+// (optional, NULL = all +1) a length-n vector: block b uses signs[1024b ..]
+// (the host form, src/fwht.h:38-42).  Stage order h = 1..512 as the host, so
+// the result is bit-identical to fwht_blocks().  Errors: 1 if n <= 0 or
+// n % 1024 != 0.  Replaces include/bonsai_p40.h:41 (elementwise_p40.cu:75-80).
+int bonsai_p40_fwht(float * x, const float * signs, int64_t n, bonsai_stream stream);
+
+// Not on the PQ2_0 matmul path; kept so the reference's symbol set links.
+// rmsnorm: y = x * (1/sqrt(mean(x^2) + eps)) * w per row (src/ops.h:13-22).
+int bonsai_p40_rmsnorm(const float * x, const float * w, float * y,
+                       int64_t n_rows, int64_t n, float eps, bonsai_stream stream);
+// gdn_step / attn are outside this library's scope: they return 2
+// ("not implemented") without touching memory.
+int bonsai_p40_gdn_step(float * state, const float * q, const float * k, const float * v,
+                        const float * g, const float * beta, float * out,
+                        int n_k_heads, int n_v_heads, int K, int V, bonsai_stream stream);
+int bonsai_p40_attn(const float * q, const float * k, const float * v, float * out,
+                    int n_tok, int n_head, int n_head_kv, int head_dim, float scale,
+                    bonsai_stream stream);
+
+// --- additions (no counterpart in the reference header) -------------------------
+// Fused decode pre-pass: xq = Q8_1(FWHT(signs .* x)) for one token of n floats
+// (x is not modified).  One launch in place of bonsai_p40_fwht followed by
+// bonsai_p40_quant_activations (elementwise_p40.cu:17-41 + gemv_p40.cu:168-196),
+// bit-identical to the host fwht_blocks + quantize_row_q8_1(permute = true).
+// Errors: 1 if n <= 0 or n % 1024 != 0.
+int bonsai_p40_fwht_quant(const float * x, const float * signs, void * xq, int64_t n,
+                          bonsai_stream stream);
+
+// Batched pre-pass for the GEMM: X is [n_tok][n] fp32 (token rows); each token
+// is optionally rotated (rotate != 0: FWHT with signs, n % 1024 == 0) and
+// quantised on its own, written chunk-major (block (c, t) at c*n_tok + t) --
+// the Xq layout bonsai_p40_gemm consumes, which the reference API has no
+// producer for.  Errors: 1 if n <= 0, n % 32 != 0 (n % 1024 with rotate) or
+// n_tok <= 0.
+int bonsai_p40_quant_tokens(const float * X, const float * signs, void * Xq, int64_t n,
+                            int64_t n_tok, int rotate, bonsai_stream stream);
+
+// FFN glue of the decode chain: xq = Q8_1(FWHT(signs .* (silu(gate) * up)))
+// with silu(g) = g / (1 + exp(-g)) (src/ops.h:27-31), one launch.
+// Errors: 1 if n <= 0 or n % 1024 != 0.
+int bonsai_p40_swiglu_fwht_quant(const float * gate, const float * up, const float * signs,
+                                 void * xq, int64_t n, bonsai_stream stream);
+
+// Test hook: out[r * (n_in/32) + c] = the int32 chunk dot sum_k (code-1)*q of
+// row r, chunk c, computed by the same device code path as bonsai_p40_gemv
+// (the value of src/pq2_0.h:149-177 before scaling).  Errors as bonsai_p40_gemv.
+int bonsai_p40_chunk_dots(const void * W, const void * xq, int32_t * out,
+                          int64_t n_out, int64_t n_in, bonsai_stream stream);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,153 @@
+"""Host-side Python binding of libbonsai_p40.so (the gfx950 PQ2_0 matmul path).
+
+The native library exports the C ABI of include/bonsai_p40.h; this module
+binds it with ctypes and offers thin wrappers over torch device tensors
+(torch is used only for device memory and the current HIP stream).  Every
+wrapper raises if the library is missing or a call returns nonzero -- there is
+no CPU fallback in this module.
+
+Reference interface mirrored: include/bonsai_p40.h of boetti-dev/p40-kernel
+(bonsai_p40_gemv, _quant_activations, _gemm, _repack, _gemv_repack, _fwht,
+_rmsnorm), plus the additions declared at the end of the header.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libbonsai_p40.so")
+
+QK_PQ2 = 128          # weights per block_pq2_0
+QK8 = 32              # elements per block_q8_1
+PQ2_BYTES = 34        # sizeof(block_pq2_0)
+Q81_BYTES = 36        # sizeof(block_q8_1)
+HBLK = 1024           # Hadamard block
+
+# Every symbol of include/bonsai_p40.h with its ctypes signature.
+_V, _I64, _F32P = C.c_void_p, C.c_int64, C.c_void_p
+SIGNATURES = {
+    "bonsai_p40_gemv": [_V, _V, _F32P, _I64, _I64, _V],
+    "bonsai_p40_quant_activations": [_F32P, _V, _I64, _V],
+    "bonsai_p40_gemm": [_V, _V, _F32P, _I64, _I64, _I64, _V],
+    "bonsai_p40_repack": [_V, _V, _I64, _I64, _V],
+    "bonsai_p40_gemv_repack": [_V, _F32P, _F32P, _I64, _I64, _V],
+    "bonsai_p40_fwht": [_F32P, _F32P, _I64, _V],
+    "bonsai_p40_rmsnorm": [_F32P, _F32P, _F32P, _I64, _I64, C.c_float, _V],
+    "bonsai_p40_gdn_step": [_F32P] * 7 + [C.c_int] * 4 + [_V],
+    "bonsai_p40_attn": [_F32P] * 4 + [C.c_int] * 4 + [C.c_float, _V],
+    "bonsai_p40_fwht_quant": [_F32P, _F32P, _V, _I64, _V],
+    "bonsai_p40_quant_tokens": [_F32P, _F32P, _V, _I64, _I64, C.c_int, _V],
+    "bonsai_p40_swiglu_fwht_quant": [_F32P, _F32P, _F32P, _V, _I64, _V],
+    "bonsai_p40_chunk_dots": [_V, _V, _V, _I64, _I64, _V],
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """Load libbonsai_p40.so; raise if it was not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `make -C p40-kernel_amd` "
+                "(or __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = argtypes
+            fn.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+class BonsaiError(RuntimeError):
+    pass
+
+
+def _check(name: str, rc: int) -> None:
+    if rc != 0:
+        raise BonsaiError(f"{name} returned {rc}")
+
+
+def _ptr(t) -> int | None:
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is not None:
+        return stream if isinstance(stream, int) else stream.cuda_stream
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def call(name: str, *args, stream=None) -> int:
+    """Raw call: tensors are passed as device pointers; returns the rc."""
+    fn = getattr(lib(), name)
+    conv = [_ptr(a) if (a is None or hasattr(a, "data_ptr")) else a for a in args]
+    return fn(*conv, _stream(stream))
+
+
+# -------------------------------------------------------------- wrappers
+def gemv(W, xq, y, n_out: int, n_in: int, stream=None) -> None:
+    _check("bonsai_p40_gemv", call("bonsai_p40_gemv", W, xq, y, n_out, n_in, stream=stream))
+
+
+def quant_activations(x, out, n: int, stream=None) -> None:
+    _check("bonsai_p40_quant_activations",
+           call("bonsai_p40_quant_activations", x, out, n, stream=stream))
+
+
+def gemm(W, Xq, Y, n_out: int, n_in: int, n_tok: int, stream=None) -> None:
+    _check("bonsai_p40_gemm", call("bonsai_p40_gemm", W, Xq, Y, n_out, n_in, n_tok, stream=stream))
+
+
+def repack(src, dst, n_out: int, n_in: int, stream=None) -> None:
+    _check("bonsai_p40_repack", call("bonsai_p40_repack", src, dst, n_out, n_in, stream=stream))
+
+
+def gemv_repack(W, x, y, n_out: int, n_in: int, stream=None) -> None:
+    _check("bonsai_p40_gemv_repack",
+           call("bonsai_p40_gemv_repack", W, x, y, n_out, n_in, stream=stream))
+
+
+def fwht(x, signs, n: int, stream=None) -> None:
+    _check("bonsai_p40_fwht", call("bonsai_p40_fwht", x, signs, n, stream=stream))
+
+
+def rmsnorm(x, w, y, n_rows: int, n: int, eps: float, stream=None) -> None:
+    _check("bonsai_p40_rmsnorm",
+           call("bonsai_p40_rmsnorm", x, w, y, n_rows, n, C.c_float(eps), stream=stream))
+
+
+def fwht_quant(x, signs, xq, n: int, stream=None) -> None:
+    _check("bonsai_p40_fwht_quant", call("bonsai_p40_fwht_quant", x, signs, xq, n, stream=stream))
+
+
+def quant_tokens(X, signs, Xq, n: int, n_tok: int, rotate: bool, stream=None) -> None:
+    _check("bonsai_p40_quant_tokens",
+           call("bonsai_p40_quant_tokens", X, signs, Xq, n, n_tok, int(rotate), stream=stream))
+
+
+def swiglu_fwht_quant(gate, up, signs, xq, n: int, stream=None) -> None:
+    _check("bonsai_p40_swiglu_fwht_quant",
+           call("bonsai_p40_swiglu_fwht_quant", gate, up, signs, xq, n, stream=stream))
+
+
+def chunk_dots(W, xq, out, n_out: int, n_in: int, stream=None) -> None:
+    _check("bonsai_p40_chunk_dots",
+           call("bonsai_p40_chunk_dots", W, xq, out, n_out, n_in, stream=stream))
+
+
+# --------------------------------------------------------- sizes / helpers
+def pq2_bytes(n_out: int, n_in: int) -> int:
+    return n_out * (n_in // QK_PQ2) * PQ2_BYTES
+
+
+def q8_bytes(n: int, n_tok: int = 1) -> int:
+    return n // QK8 * n_tok * Q81_BYTES

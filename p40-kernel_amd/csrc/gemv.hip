@@ -1,0 +1,305 @@
+// gemv.hip -- decode GEMV over the native 34-byte block_pq2_0 layout (gfx950).
+//
+// Contract: y[r] = sum_b sum_iqs (f16(d_w) * f16(d_a)) * sumi(r, b, iqs) where
+// sumi = sum_k dot4((w >> 2k) & 0x03030303, a_k) - s is the integer chunk dot
+// of src/pq2_0.h:149-191; replaces src/kernels/gemv_p40.cu:82-165,210-219.
+// Integer chunk dots are exact; the fp32 sum is a lane-parallel tree instead
+// of the host's sequential loop (compared within 1e-5 relative, normwise).
+//
+// Streaming design (fast path: n_in % 1024 == 0, W 16-byte aligned)
+// ---------------------------------------------------------------------
+// * Rows are contiguous runs of 34*nb bytes and nb % 8 == 0, so every row
+//   starts 16-byte aligned.  A wave owns a "unit" of G consecutive rows
+//   (G = 2 when 4*nb % 64 == 32, else 1) = G*34*nb contiguous bytes, and
+//   streams it with fully coalesced 128-bit loads (64 lanes x 16 B = 1 KiB per
+//   instruction) into registers, then into its private LDS buffer.  The next
+//   unit's loads are in flight while the current unit is consumed.
+// * In LDS the unit is read as a sequence of "slots" of 64 chunks (16 blocks,
+//   544 bytes): lane l takes chunk 64j + l of slot j.  Since 4*nb*G is a
+//   multiple of 64, every slot is full; with G = 2 one slot straddles the two
+//   rows exactly at lane 32.  The lane's 8 code bytes start 2 bytes past a
+//   dword boundary for even blocks, so it reads 3 aligned dwords and realigns
+//   with v_alignbyte (a per-lane constant shift).
+// * The permuted Q8_1 activation is staged once per workgroup into LDS as a
+//   16-byte aligned plane of int8 words plus a {d_a as f32, -s} plane; each
+//   slot reads its chunk's 8 words with two ds_read_b128.
+// * The chunk dot is 8 v_dot4 with the -s bias as the accumulator seed; the
+//   fp32 row partials are reduced across the wave with DPP (quad_perm,
+//   row_half_mirror, row_mirror, row_bcast15/31) and lane 63 stores y.
+// Any other shape or alignment takes a simple wave-per-row kernel.
+#include "pq2_device.h"
+#include "../../include/bonsai_p40.h"
+
+#include <stdlib.h>
+
+using namespace pq2;
+
+namespace {
+
+constexpr int GV_WAVES = 4;
+constexpr int GV_THREADS = 64 * GV_WAVES;
+constexpr int SLOT_BYTES = 16 * PQ2_BYTES;   // 64 chunks = 16 blocks = 544 B
+constexpr int MAX_NPL = 17;                  // max 16-byte pieces per lane per unit
+
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+struct StreamGeom {
+    int nb, nchunk, G, unit_bytes, ubuf_pad, slots, npieces, npl;
+    size_t lds_bytes;
+};
+
+inline StreamGeom stream_geom(int64_t n_in) {
+    StreamGeom g{};
+    g.nb = (int)(n_in / QK_PQ2);
+    g.nchunk = 4 * g.nb;
+    g.G = (g.nchunk % 64 == 0) ? 1 : 2;
+    g.unit_bytes = g.G * PQ2_BYTES * g.nb;
+    g.ubuf_pad = g.unit_bytes + 16;
+    g.slots = g.G * g.nchunk / 64;
+    g.npieces = g.unit_bytes / 16;
+    g.npl = (g.npieces + 63) / 64;
+    g.lds_bytes = (size_t)g.nchunk * 40 + (size_t)GV_WAVES * g.ubuf_pad;
+    return g;
+}
+
+// Stage the permuted Q8_1 activation (36-byte blocks, 4-byte aligned) into
+// LDS: act_q[c*8 + k] = activation word k of chunk c, act_sc[c] = {d_a, -s}.
+__device__ __forceinline__ void stage_activation(const uint32_t * __restrict__ xw,
+                                                 uint32_t * act_q, int2 * act_sc, int nchunk) {
+    for (int m = threadIdx.x; m < nchunk * 9; m += blockDim.x) {
+        const uint32_t v = xw[m];
+        const int c = m / 9, k = m - 9 * c;
+        if (k == 0)
+            act_sc[c] = make_int2(__float_as_int(f16_bits_to_f32(v & 0xffffu)), -(int)(int16_t)(v >> 16));
+        else
+            act_q[8 * c + k - 1] = v;
+    }
+}
+
+template <int G, int NPL, bool DUMP>
+__global__ void __launch_bounds__(GV_THREADS)
+gemv_stream_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
+                   float * __restrict__ y, int32_t * __restrict__ dump, int n_out, int nb,
+                   int units_per_wave) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int nchunk = 4 * nb;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    uint32_t * act_q = reinterpret_cast<uint32_t *>(smem);
+    int2 * act_sc = reinterpret_cast<int2 *>(smem + (size_t)nchunk * 32);
+    const int unit_bytes = G * PQ2_BYTES * nb;
+    uint8_t * ubuf = smem + (size_t)nchunk * 40 + (size_t)wave * (unit_bytes + 16);
+
+    stage_activation(reinterpret_cast<const uint32_t *>(xq), act_q, act_sc, nchunk);
+    __syncthreads();
+
+    const int n_units = (n_out + G - 1) / G;
+    int u = (blockIdx.x * GV_WAVES + wave) * units_per_wave;
+    const int u_end = min(u + units_per_wave, n_units);
+    if (u >= u_end) return;   // no workgroup barrier below this point
+
+    const size_t total_bytes = (size_t)n_out * PQ2_BYTES * nb;
+    const int npieces = unit_bytes / 16;
+    const int slots = G * nchunk / 64;
+
+    // per-lane constants of the slot walk
+    const int cw = PQ2_BYTES * (lane >> 2) + 2 + 8 * (lane & 3);   // code bytes of chunk `lane`
+    const int sh = cw & 3;                                           // 2 (even block) or 0
+    const int cw_al = cw - sh;
+    const int dwo = PQ2_BYTES * (lane >> 2);                         // fp16 d of its block
+
+    v4u r[NPL];
+    auto load_unit = [&](int uu) {
+        const uint8_t * src = W + (size_t)uu * unit_bytes;
+        const size_t avail = total_bytes - (size_t)uu * unit_bytes;
+#pragma unroll
+        for (int k = 0; k < NPL; ++k) {
+            const int p = lane + 64 * k;
+            if (p < npieces && (size_t)16 * p < avail)
+                r[k] = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(src) + p);
+        }
+    };
+
+    load_unit(u);
+    for (; u < u_end; ++u) {
+#pragma unroll
+        for (int k = 0; k < NPL; ++k) {
+            const int p = lane + 64 * k;
+            if (p < npieces) *reinterpret_cast<v4u *>(ubuf + 16 * p) = r[k];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (u + 1 < u_end) load_unit(u + 1);
+
+        float acc0 = 0.0f, acc1 = 0.0f;
+        for (int j = 0; j < slots; ++j) {
+            const uint8_t * cp = ubuf + cw_al + SLOT_BYTES * j;
+            const uint32_t d0 = *reinterpret_cast<const uint32_t *>(cp);
+            const uint32_t d1 = *reinterpret_cast<const uint32_t *>(cp + 4);
+            const uint32_t d2 = *reinterpret_cast<const uint32_t *>(cp + 8);
+            const uint32_t w0 = __builtin_amdgcn_alignbyte(d1, d0, sh);
+            const uint32_t w1 = __builtin_amdgcn_alignbyte(d2, d1, sh);
+            const uint32_t dwb = *reinterpret_cast<const uint16_t *>(ubuf + dwo + SLOT_BYTES * j);
+            const int v = 64 * j + lane;
+            const bool second = (G == 2) && (v >= nchunk);
+            const int c = second ? v - nchunk : v;
+            const int4 a0 = *reinterpret_cast<const int4 *>(act_q + 8 * c);
+            const int4 a1 = *reinterpret_cast<const int4 *>(act_q + 8 * c + 4);
+            const int2 sc = act_sc[c];
+            const int a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            const int s = chunk_dot_i32(w0, w1, a, sc.y);
+            if (DUMP) {
+                const int row = u * G + (second ? 1 : 0);
+                if (row < n_out) dump[(size_t)row * nchunk + c] = s;
+            } else {
+                const float contrib = f16_bits_to_f32(dwb) * (__int_as_float(sc.x) * (float)s);
+                if (second) acc1 += contrib; else acc0 += contrib;
+            }
+        }
+        if (!DUMP) {
+            const float t0 = wave_sum_to_lane63(acc0);
+            const int row0 = u * G;
+            if (lane == 63) y[row0] = t0;
+            if (G == 2) {
+                const float t1 = wave_sum_to_lane63(acc1);
+                if (lane == 63 && row0 + 1 < n_out) y[row0 + 1] = t1;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
+// Generic path: one wave per row, lane-strided chunks, 2-byte weight loads
+// (any n_in % 128 == 0, any 2-byte aligned W).
+template <bool DUMP>
+__global__ void __launch_bounds__(GV_THREADS)
+gemv_rowwave_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
+                    float * __restrict__ y, int32_t * __restrict__ dump, int n_out, int nb) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * GV_WAVES + (threadIdx.x >> 6);
+    if (row >= n_out) return;
+    const int nchunk = 4 * nb;
+    const uint8_t * wr = W + (size_t)row * PQ2_BYTES * nb;
+    float acc = 0.0f;
+    for (int c = lane; c < nchunk; c += 64) {
+        const uint8_t * blk = wr + (size_t)PQ2_BYTES * (c >> 2);
+        const uint16_t * qp = reinterpret_cast<const uint16_t *>(blk + 2 + 8 * (c & 3));
+        const uint32_t w0 = (uint32_t)qp[0] | ((uint32_t)qp[1] << 16);
+        const uint32_t w1 = (uint32_t)qp[2] | ((uint32_t)qp[3] << 16);
+        const uint32_t * ab = reinterpret_cast<const uint32_t *>(xq + (size_t)Q81_BYTES * c);
+        const uint32_t ds = ab[0];
+        const int a[8] = {(int)ab[1], (int)ab[2], (int)ab[3], (int)ab[4],
+                          (int)ab[5], (int)ab[6], (int)ab[7], (int)ab[8]};
+        const int s = chunk_dot_i32(w0, w1, a, -(int)(int16_t)(ds >> 16));
+        if (DUMP) {
+            dump[(size_t)row * nchunk + c] = s;
+        } else {
+            const float dw = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(blk));
+            acc += dw * (f16_bits_to_f32(ds & 0xffffu) * (float)s);
+        }
+    }
+    if (!DUMP) {
+        acc = wave_sum_to_lane63(acc);
+        if (lane == 63) y[row] = acc;
+    }
+}
+
+int env_int(const char * name, int dflt) {
+    const char * s = getenv(name);
+    return (s && *s) ? atoi(s) : dflt;
+}
+
+int max_lds_per_block() {
+    static int v = -1;
+    if (v < 0) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        int x = 0;
+        if (hipDeviceGetAttribute(&x, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || x <= 0)
+            x = 64 * 1024;
+        v = x;
+    }
+    return v;
+}
+
+template <int G, int NPL, bool DUMP>
+int launch_stream_t(const uint8_t * W, const uint8_t * xq, float * y, int32_t * dump, int n_out,
+                    const StreamGeom & g, hipStream_t st) {
+    auto kern = gemv_stream_kernel<G, NPL, DUMP>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, max_lds_per_block());
+        attr_set = true;
+    }
+    const int n_units = (n_out + G - 1) / G;
+    int upw = env_int("BONSAI_GEMV_UNITS_PER_WAVE", 0);
+    if (upw <= 0) {
+        const int target_waves = 256 * 12;
+        upw = (n_units + target_waves - 1) / target_waves;
+        if (upw < 1) upw = 1;
+    }
+    const int waves = (n_units + upw - 1) / upw;
+    const int blocks = (waves + GV_WAVES - 1) / GV_WAVES;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(GV_THREADS), g.lds_bytes, st, W, xq, y, dump,
+                       n_out, g.nb, upw);
+    return (int)hipGetLastError();
+}
+
+template <int G, bool DUMP>
+int launch_stream_g(const uint8_t * W, const uint8_t * xq, float * y, int32_t * dump, int n_out,
+                    const StreamGeom & g, hipStream_t st) {
+    switch (g.npl) {
+#define PQ2_NPL_CASE(N) case N: return launch_stream_t<G, N, DUMP>(W, xq, y, dump, n_out, g, st);
+        PQ2_NPL_CASE(1) PQ2_NPL_CASE(2) PQ2_NPL_CASE(3) PQ2_NPL_CASE(4) PQ2_NPL_CASE(5)
+        PQ2_NPL_CASE(6) PQ2_NPL_CASE(7) PQ2_NPL_CASE(8) PQ2_NPL_CASE(9) PQ2_NPL_CASE(10)
+        PQ2_NPL_CASE(11) PQ2_NPL_CASE(12) PQ2_NPL_CASE(13) PQ2_NPL_CASE(14) PQ2_NPL_CASE(15)
+        PQ2_NPL_CASE(16) PQ2_NPL_CASE(17)
+#undef PQ2_NPL_CASE
+        default: return -1;
+    }
+}
+
+template <bool DUMP>
+int gemv_dispatch(const void * W, const void * xq, float * y, int32_t * dump, int64_t n_out,
+                  int64_t n_in, hipStream_t st) {
+    const uint8_t * w = static_cast<const uint8_t *>(W);
+    const uint8_t * x = static_cast<const uint8_t *>(xq);
+    if (n_out > 0x7fffffff || n_in / QK_PQ2 > (1 << 24)) return 1;
+    const StreamGeom g = stream_geom(n_in);
+    const bool fast = (n_in % HBLK == 0) && (((uintptr_t)w & 15u) == 0) && g.npl <= MAX_NPL &&
+                      g.lds_bytes <= (size_t)max_lds_per_block() &&
+                      env_int("BONSAI_GEMV_GENERIC", 0) == 0;
+    if (fast) {
+        const int rc = (g.G == 1) ? launch_stream_g<1, DUMP>(w, x, y, dump, (int)n_out, g, st)
+                                  : launch_stream_g<2, DUMP>(w, x, y, dump, (int)n_out, g, st);
+        if (rc >= 0) return rc;
+    }
+    const unsigned blocks = (unsigned)((n_out + GV_WAVES - 1) / GV_WAVES);
+    hipLaunchKernelGGL(gemv_rowwave_kernel<DUMP>, dim3(blocks), dim3(GV_THREADS), 0, st, w, x, y,
+                       dump, (int)n_out, g.nb);
+    return (int)hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" {
+
+int bonsai_p40_gemv(const void * W, const void * xq, float * y, int64_t n_out, int64_t n_in,
+                    bonsai_stream stream) {
+    if (n_in <= 0 || n_in % QK_PQ2 != 0 || ((uintptr_t)xq & 3u) != 0) return 1;
+    if (n_out <= 0) return 0;
+    return gemv_dispatch<false>(W, xq, y, nullptr, n_out, n_in, (hipStream_t)stream);
+}
+
+int bonsai_p40_chunk_dots(const void * W, const void * xq, int32_t * out, int64_t n_out,
+                          int64_t n_in, bonsai_stream stream) {
+    if (n_in <= 0 || n_in % QK_PQ2 != 0 || ((uintptr_t)xq & 3u) != 0) return 1;
+    if (n_out <= 0) return 0;
+    return gemv_dispatch<true>(W, xq, nullptr, out, n_out, n_in, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,105 @@
+// pq2_device.h -- gfx950 device helpers shared by the PQ2_0 kernels.
+//
+// Formats (reference src/pq2_0.h:45-54): block_pq2_0 is 34 bytes (fp16 d at
+// byte 0, 32 code bytes at 2), block_q8_1 is 36 bytes (fp16 d at 0, raw int16
+// activation sum s at 2, 32 permuted int8 at 4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pq2 {
+
+constexpr int QK_PQ2 = 128;      // weights per PQ2_0 block
+constexpr int QK8 = 32;          // elements per Q8_1 block
+constexpr int PQ2_BYTES = 34;
+constexpr int Q81_BYTES = 36;
+constexpr int HBLK = 1024;       // Hadamard block
+
+// ---- fp16 ----------------------------------------------------------------
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// fp32 -> fp16 bits with the reference HOST rounding (src/p40_common.h:82-114):
+// the magnitude rounds half away from zero (hardware cvt rounds to nearest
+// even, which differs on exact ties), overflow -> inf, NaN -> quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_f16_away(float f) {
+    const uint32_t x = __float_as_uint(f);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t fe = (x >> 23) & 0xffu;
+    const uint32_t mant = x & 0x7fffffu;
+    int e = (int)fe - 112;
+    if (fe == 0xffu) return sign | 0x7c00u | (mant ? 0x200u : 0u);
+    if (e >= 31) return sign | 0x7c00u;
+    if (e <= 0) {
+        if (e < -10) return sign;
+        const uint32_t full = mant | 0x800000u;
+        const uint32_t sh = (uint32_t)(14 - e);
+        uint32_t q = full >> sh;
+        q += (full >> (sh - 1)) & 1u;
+        return sign | q;
+    }
+    uint32_t q = mant >> 13;
+    if (mant & 0x1000u) {
+        ++q;
+        if (q == 0x400u) { q = 0; ++e; if (e >= 31) return sign | 0x7c00u; }
+    }
+    return sign | ((uint32_t)e << 10) | q;
+}
+
+// ---- DPP cross-lane helpers (wave64) --------------------------------------
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK,
+                                                      BANK_MASK, false));
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+
+constexpr int DPP_QUAD_XOR1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;
+constexpr int DPP_ROW_MIRROR = 0x140;
+constexpr int DPP_ROW_BCAST15 = 0x142;
+constexpr int DPP_ROW_BCAST31 = 0x143;
+
+// Sum over the 64 lanes of a wave; the total lands in lane 63.
+// Rows of 16 are reduced with quad/mirror DPP moves (every lane of a row then
+// holds the row sum), then row_bcast:15 / row_bcast:31 fold the four rows
+// into lane 63.
+__device__ __forceinline__ float wave_sum_to_lane63(float v) {
+    v += dpp_mov<DPP_QUAD_XOR1>(v);
+    v += dpp_mov<DPP_QUAD_XOR2>(v);
+    v += dpp_mov<DPP_ROW_HALF_MIRROR>(v);
+    v += dpp_mov<DPP_ROW_MIRROR>(v);
+    v += dpp_mov<DPP_ROW_BCAST15, 0xa>(v);
+    v += dpp_mov<DPP_ROW_BCAST31, 0xc>(v);
+    return v;
+}
+
+// ---- integer chunk dot ------------------------------------------------------
+// sumi = bias + sum_k dot4((w >> 2k) & 0x03030303, a_k) over the two 16-code
+// words (w0, w1) of a 32-weight chunk against the 8 permuted activation words
+// (src/pq2_0.h:149-172).  Codes are 0..3, so the signed v_dot4 equals the
+// reference's unsigned-code x signed-activation product.
+__device__ __forceinline__ int chunk_dot_i32(uint32_t w0, uint32_t w1, const int (&a)[8],
+                                             int bias) {
+    int s = bias;
+    s = __builtin_amdgcn_sdot4((int)(w0 & 0x03030303u), a[0], s, false);
+    s = __builtin_amdgcn_sdot4((int)((w0 >> 2) & 0x03030303u), a[1], s, false);
+    s = __builtin_amdgcn_sdot4((int)((w0 >> 4) & 0x03030303u), a[2], s, false);
+    s = __builtin_amdgcn_sdot4((int)((w0 >> 6) & 0x03030303u), a[3], s, false);
+    s = __builtin_amdgcn_sdot4((int)(w1 & 0x03030303u), a[4], s, false);
+    s = __builtin_amdgcn_sdot4((int)((w1 >> 2) & 0x03030303u), a[5], s, false);
+    s = __builtin_amdgcn_sdot4((int)((w1 >> 4) & 0x03030303u), a[6], s, false);
+    s = __builtin_amdgcn_sdot4((int)((w1 >> 6) & 0x03030303u), a[7], s, false);
+    return s;
+}
+
+__host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace pq2

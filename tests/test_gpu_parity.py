@@ -1,0 +1,342 @@
+"""GPU parity tests: the HIP path (through the C ABI) against the CPU oracle.
+
+Bars (from the reference host code, src/pq2_0.h, src/fwht.h, tests/test_p40.cpp):
+  * Q8_1 bytes, repacked bytes, int32 chunk dots, FWHT fp32 bits: exact;
+  * fp32 GEMV/GEMM outputs: max |dy| <= 1e-5 * max |y_ref| (normwise; the
+    device sums chunks in a different order than the host's sequential loop);
+  * chains containing expf (SwiGLU): 1e-4 normwise, since device and glibc
+    expf differ in the last ulp.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import bonsai_p40 as B
+from oracle import oracle as O
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    B.lib()   # fail loudly if the native library is missing
+    yield
+    torch.cuda.synchronize()
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def dev(a: np.ndarray):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def normwise(got, ref):
+    scale = max(float(np.max(np.abs(ref))), 1e-30)
+    return float(np.max(np.abs(got.astype(np.float64) - ref.astype(np.float64)))) / scale
+
+
+def offset_copy(a: np.ndarray, offset: int):
+    """Device copy of a byte array starting `offset` bytes past a 256-B boundary."""
+    buf = torch.zeros(a.size + 64, dtype=torch.uint8, device="cuda")
+    buf[offset:offset + a.size] = dev(a)
+    return buf, buf.data_ptr() + offset
+
+
+# ------------------------------------------------------------------ FWHT
+def test_fwht_fixture_bits(golden):
+    case("fwht n=2048 fixture, signs None / length-n")
+    x = dev(golden["f3_in"])
+    B.fwht(x, None, 2048)
+    assert np.array_equal(bits(host(x)), bits(golden["f3_out"]))
+    x = dev(golden["f3_in"])
+    B.fwht(x, dev(golden["f3_signs"]), 2048)
+    assert np.array_equal(bits(host(x)), bits(golden["f3_out_signed"]))
+
+
+@pytest.mark.parametrize("n,offset", [(5120, 0), (17408, 0), (17408, 1), (1024, 3)])
+def test_fwht_seeded_bits(n, offset):
+    case(f"fwht n={n} float offset={offset}")
+    x = O.gen_normal(300 + n, n)
+    s = np.where(O.gen_normal(301 + n, n) > 0, 1.0, -1.0).astype(np.float32)
+    buf = torch.zeros(n + 8, dtype=torch.float32, device="cuda")
+    buf[offset:offset + n] = dev(x)
+    B.fwht(buf.data_ptr() + 4 * offset, dev(s), n)
+    assert np.array_equal(bits(host(buf)[offset:offset + n]), bits(O.fwht(x, s)))
+
+
+# ------------------------------------------------------------- quantisers
+@pytest.mark.parametrize("name", ["seeded", "special", "k32"])
+def test_quant_activations_fixture(golden, name):
+    case(f"quant_activations fixture {name}")
+    x = golden[f"f2_{name}_in"]
+    q = torch.zeros(x.size // 32 * 36, dtype=torch.uint8, device="cuda")
+    B.quant_activations(dev(x), q, x.size)
+    np.testing.assert_array_equal(host(q), golden[f"f2_{name}_perm"])
+
+
+@pytest.mark.parametrize("n", [32, 96, 5120, 17408, 32768])
+def test_quant_activations_seeded(n):
+    case(f"quant_activations n={n}")
+    x = O.gen_normal(400 + n, n) * 2.5
+    q = torch.zeros(n // 32 * 36, dtype=torch.uint8, device="cuda")
+    B.quant_activations(dev(x), q, n)
+    np.testing.assert_array_equal(host(q), O.quantize_q8_1(x, True))
+
+
+@pytest.mark.parametrize("n,signed", [(5120, False), (5120, True), (17408, True), (6144, False)])
+def test_fwht_quant_bytes(n, signed):
+    case(f"fwht_quant n={n} signed={signed}")
+    x = O.gen_normal(500 + n, n)
+    s = np.where(O.gen_normal(501 + n, n) > 0, 1.0, -1.0).astype(np.float32) if signed else None
+    q = torch.zeros(n // 32 * 36, dtype=torch.uint8, device="cuda")
+    B.fwht_quant(dev(x), None if s is None else dev(s), q, n)
+    np.testing.assert_array_equal(host(q), O.quantize_q8_1(O.fwht(x, s), True))
+
+
+@pytest.mark.parametrize("n,n_tok,rotate", [(1024, 5, True), (5120, 64, True), (256, 5, False),
+                                            (5120, 3, False)])
+def test_quant_tokens_chunk_major(n, n_tok, rotate):
+    case(f"quant_tokens n={n} n_tok={n_tok} rotate={rotate}")
+    X = O.gen_normal(600 + n + n_tok, n * n_tok).reshape(n_tok, n)
+    q = torch.zeros(n // 32 * n_tok * 36, dtype=torch.uint8, device="cuda")
+    B.quant_tokens(dev(X), None, q, n, n_tok, rotate)
+    Xr = np.stack([O.fwht(X[t]) for t in range(n_tok)]) if rotate else X
+    np.testing.assert_array_equal(host(q), O.quantize_chunk_major(Xr))
+
+
+def test_swiglu_fwht_quant_fixture(golden):
+    case("swiglu_fwht_quant n=2048 fixture")
+    q = torch.zeros(2048 // 32 * 36, dtype=torch.uint8, device="cuda")
+    B.swiglu_fwht_quant(dev(golden["f7_gate"]), dev(golden["f7_up"]), None, q, 2048)
+    got = host(q)
+    ref = golden["f7_hq"]
+    d1, s1, q1 = O.q81_fields(got)
+    d2, s2, q2 = O.q81_fields(ref)
+    # device expf may differ from glibc in the last ulp: q bytes may move by 1
+    assert np.max(np.abs(q1.astype(int) - q2.astype(int))) <= 1
+    assert np.mean(q1 != q2) < 0.01
+    assert np.max(np.abs(d1.astype(int) - d2.astype(int))) <= 1
+
+
+# --------------------------------------------------------- chunk dots / GEMV
+SHAPES = [
+    (8, 5120), (5, 5120), (1, 5120), (64, 17408), (33, 6144), (7, 1024), (9, 10240),
+    (6, 12288), (3, 384), (4, 128), (17, 2048),
+]
+
+
+def make(n_out, n_in, seed, p3=0.001):
+    W = O.gen_weights(seed, n_out, n_in, p3)
+    xq = O.quantize_q8_1(O.fwht(O.gen_normal(seed + 1, n_in)) if n_in % 1024 == 0
+                         else O.gen_normal(seed + 1, n_in), True)
+    return W, xq
+
+
+@pytest.mark.parametrize("k", [5120, 17408])
+def test_chunk_dots_fixture(golden, k):
+    case(f"chunk_dots fixture k={k}")
+    out = torch.zeros((8, k // 32), dtype=torch.int32, device="cuda")
+    B.chunk_dots(dev(golden[f"f4_{k}_W"]), dev(golden[f"f4_{k}_xq"]), out, 8, k)
+    np.testing.assert_array_equal(host(out), golden[f"f4_{k}_sumi"])
+
+
+@pytest.mark.parametrize("n_out,n_in", SHAPES)
+@pytest.mark.parametrize("w_offset", [0, 2])
+def test_chunk_dots_exact(n_out, n_in, w_offset):
+    case(f"chunk_dots {n_out}x{n_in} W offset {w_offset}")
+    W, xq = make(n_out, n_in, 700 + n_out + n_in, 0.05)
+    buf, wp = offset_copy(W, w_offset)
+    out = torch.full((n_out, n_in // 32), -999999, dtype=torch.int32, device="cuda")
+    B.chunk_dots(wp, dev(xq), out, n_out, n_in)
+    np.testing.assert_array_equal(host(out), O.chunk_dots(W, xq, n_out, n_in))
+
+
+@pytest.mark.parametrize("k", [5120, 17408])
+def test_gemv_fixture(golden, k):
+    case(f"gemv fixture k={k}")
+    y = torch.zeros(8, dtype=torch.float32, device="cuda")
+    B.gemv(dev(golden[f"f4_{k}_W"]), dev(golden[f"f4_{k}_xq"]), y, 8, k)
+    assert normwise(host(y), golden[f"f4_{k}_y"]) <= TOL
+
+
+@pytest.mark.parametrize("n_out,n_in", SHAPES)
+@pytest.mark.parametrize("w_offset", [0, 2])
+def test_gemv_matches_oracle(n_out, n_in, w_offset):
+    case(f"gemv {n_out}x{n_in} W offset {w_offset}")
+    W, xq = make(n_out, n_in, 800 + n_out + n_in)
+    buf, wp = offset_copy(W, w_offset)
+    y = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+    B.gemv(wp, dev(xq), y, n_out, n_in)
+    assert normwise(host(y), O.gemv(W, xq, n_out, n_in)) <= TOL
+
+
+@pytest.mark.parametrize("n_out,n_in", [(17408, 5120), (5120, 17408), (6144, 5120), (1024, 5120),
+                                        (5120, 6144), (17407, 5120)])
+def test_gemv_model_shapes(n_out, n_in):
+    case(f"gemv model shape {n_out}x{n_in}")
+    W, xq = make(n_out, n_in, 900 + n_in)
+    y = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+    Wd = dev(W)
+    B.gemv(Wd, dev(xq), y, n_out, n_in)
+    ref = O.gemv(W, xq, n_out, n_in, nthreads=16)
+    got = host(y)
+    assert np.all(np.isfinite(got))
+    assert normwise(got, ref) <= TOL
+    # the same weights twice in a row give identical output (no state)
+    B.gemv(Wd, dev(xq), y, n_out, n_in)
+    assert np.array_equal(bits(host(y)), bits(got))
+
+
+def test_gemv_code3_and_extremes():
+    case("gemv all-code-3 rows, saturated activations")
+    n_out, n_in = 6, 2048
+    W = O.gen_weights(950, n_out, n_in, 1.0)            # every code is 3 (+2)
+    x = np.zeros(n_in, np.float32)
+    x[::7] = 1e4
+    x[1::7] = -1e4
+    xq = O.quantize_q8_1(x, True)
+    y = torch.zeros(n_out, dtype=torch.float32, device="cuda")
+    B.gemv(dev(W), dev(xq), y, n_out, n_in)
+    assert normwise(host(y), O.gemv(W, xq, n_out, n_in)) <= TOL
+    out = torch.zeros((n_out, n_in // 32), dtype=torch.int32, device="cuda")
+    B.chunk_dots(dev(W), dev(xq), out, n_out, n_in)
+    np.testing.assert_array_equal(host(out), O.chunk_dots(W, xq, n_out, n_in))
+
+
+# ------------------------------------------------------------------ repack
+@pytest.mark.parametrize("n_out,n_in", [(8, 5120), (33, 17408), (5, 1024), (16, 6144)])
+def test_repack_bytes_and_gemv_repack(n_out, n_in):
+    case(f"repack + gemv_repack {n_out}x{n_in}")
+    W = O.gen_weights(1000 + n_in, n_out, n_in, 0.01)
+    Wr = torch.zeros(W.size, dtype=torch.uint8, device="cuda")
+    B.repack(dev(W), Wr, n_out, n_in)
+    Wr_h = host(Wr)
+    np.testing.assert_array_equal(Wr_h, O.repack(W, n_out, n_in))
+    x = O.fwht(O.gen_normal(1001 + n_in, n_in)) * 1.7
+    y = torch.zeros(n_out, dtype=torch.float32, device="cuda")
+    B.gemv_repack(Wr, dev(x), y, n_out, n_in)
+    assert normwise(host(y), O.gemv_repack(Wr_h, x, n_out, n_in)) <= TOL
+
+
+def test_repack_fixture(golden):
+    case("repack fixture 8x5120")
+    Wr = torch.zeros(golden["f4_5120_W"].size, dtype=torch.uint8, device="cuda")
+    B.repack(dev(golden["f4_5120_W"]), Wr, 8, 5120)
+    np.testing.assert_array_equal(host(Wr), golden["f5_Wr"])
+
+
+# -------------------------------------------------------------------- GEMM
+@pytest.mark.parametrize("tag", ["64x256x5", "32x1024x8"])
+def test_gemm_fixture(golden, tag):
+    case(f"gemm fixture {tag}")
+    n_out, n_in, n_tok = map(int, tag.split("x"))
+    Y = torch.zeros(n_out * n_tok, dtype=torch.float32, device="cuda")
+    B.gemm(dev(golden[f"f6_{tag}_W"]), dev(golden[f"f6_{tag}_Xq"]), Y, n_out, n_in, n_tok)
+    assert normwise(host(Y), golden[f"f6_{tag}_Y"]) <= TOL
+
+
+@pytest.mark.parametrize("n_out,n_in,n_tok", [(96, 1024, 1), (130, 2048, 2), (64, 5120, 4),
+                                              (200, 1024, 8), (70, 1024, 37), (128, 5120, 128),
+                                              (33, 384, 65)])
+def test_gemm_matches_oracle(n_out, n_in, n_tok):
+    case(f"gemm {n_out}x{n_in}x{n_tok}")
+    W = O.gen_weights(1100 + n_out, n_out, n_in, 0.01)
+    X = O.gen_normal(1101 + n_tok, n_tok * n_in).reshape(n_tok, n_in)
+    Xq = O.quantize_chunk_major(X)
+    Y = torch.full((n_out, n_tok), float("nan"), dtype=torch.float32, device="cuda")
+    B.gemm(dev(W), dev(Xq), Y, n_out, n_in, n_tok)
+    assert normwise(host(Y), O.gemm(W, Xq, n_out, n_in, n_tok, nthreads=16)) <= TOL
+
+
+@pytest.mark.parametrize("n_out,n_in,n_tok", [(17408, 5120, 512), (5120, 17408, 512)])
+def test_gemm_prefill_shapes_row_sample(n_out, n_in, n_tok):
+    case(f"gemm prefill {n_out}x{n_in}x{n_tok} (oracle on a row sample)")
+    W = O.gen_weights(1200 + n_in, n_out, n_in)
+    X = np.stack([O.fwht(O.gen_normal(1201 + t, n_in)) for t in range(n_tok)])
+    Xq = O.quantize_chunk_major(X)
+    Y = torch.full((n_out, n_tok), float("nan"), dtype=torch.float32, device="cuda")
+    B.gemm(dev(W), dev(Xq), Y, n_out, n_in, n_tok)
+    got = host(Y)
+    assert np.all(np.isfinite(got))
+    rows = np.r_[0:64, n_out - 64:n_out]
+    rb = n_in // 128 * 34
+    Ws = np.concatenate([W[r * rb:(r + 1) * rb] for r in rows])
+    ref = O.gemm(Ws, Xq, rows.size, n_in, n_tok, nthreads=16)
+    assert normwise(got[rows], ref) <= TOL
+
+
+def test_gemm_equals_gemv_per_token():
+    case("gemm n_tok=3 equals three gemv")
+    n_out, n_in, n_tok = 300, 5120, 3
+    W = O.gen_weights(1300, n_out, n_in)
+    X = np.stack([O.fwht(O.gen_normal(1301 + t, n_in)) for t in range(n_tok)])
+    Xq = O.quantize_chunk_major(X)
+    Y = torch.zeros((n_out, n_tok), dtype=torch.float32, device="cuda")
+    Wd = dev(W)
+    B.gemm(Wd, dev(Xq), Y, n_out, n_in, n_tok)
+    got = host(Y)
+    for t in range(n_tok):
+        xq = O.quantize_q8_1(X[t], True)
+        y = torch.zeros(n_out, dtype=torch.float32, device="cuda")
+        B.gemv(Wd, dev(xq), y, n_out, n_in)
+        assert normwise(got[:, t], host(y)) <= 2 * TOL
+
+
+# -------------------------------------------------------- config-1 FFN chain
+def test_ffn_chain_config1():
+    case("FFN chain gate/up 17408x5120 -> swiglu_fwht_quant -> down 5120x17408")
+    n_embd, n_ff = 5120, 17408
+    Wg = O.gen_weights(1400, n_ff, n_embd)
+    Wu = O.gen_weights(1401, n_ff, n_embd)
+    Wd = O.gen_weights(1402, n_embd, n_ff)
+    x = O.gen_normal(1403, n_embd)
+    xq = torch.zeros(n_embd // 32 * 36, dtype=torch.uint8, device="cuda")
+    B.fwht_quant(dev(x), None, xq, n_embd)
+    g = torch.zeros(n_ff, dtype=torch.float32, device="cuda")
+    u = torch.zeros(n_ff, dtype=torch.float32, device="cuda")
+    B.gemv(dev(Wg), xq, g, n_ff, n_embd)
+    B.gemv(dev(Wu), xq, u, n_ff, n_embd)
+    hq = torch.zeros(n_ff // 32 * 36, dtype=torch.uint8, device="cuda")
+    B.swiglu_fwht_quant(g, u, None, hq, n_ff)
+    y = torch.zeros(n_embd, dtype=torch.float32, device="cuda")
+    B.gemv(dev(Wd), hq, y, n_embd, n_ff)
+    # oracle chain
+    xq_o = O.quantize_q8_1(O.fwht(x), True)
+    assert np.array_equal(host(xq), xq_o)
+    g_o = O.gemv(Wg, xq_o, n_ff, n_embd, 16)
+    u_o = O.gemv(Wu, xq_o, n_ff, n_embd, 16)
+    assert normwise(host(g), g_o) <= TOL and normwise(host(u), u_o) <= TOL
+    hq_o = O.quantize_q8_1(O.fwht(O.swiglu(g_o, u_o)), True)
+    y_o = O.gemv(Wd, hq_o, n_embd, n_ff, 16)
+    assert normwise(host(y), y_o) <= 1e-4
+
+
+# ----------------------------------------------------------------- rmsnorm
+def test_rmsnorm():
+    case("rmsnorm 3x5120")
+    n_rows, n = 3, 5120
+    x = O.gen_normal(1500, n_rows * n).reshape(n_rows, n)
+    w = O.gen_normal(1501, n) * 0.1 + 1
+    y = torch.zeros((n_rows, n), dtype=torch.float32, device="cuda")
+    B.rmsnorm(dev(x), dev(w), y, n_rows, n, 1e-6)
+    ref = x / np.sqrt((x.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6) * w
+    np.testing.assert_allclose(host(y), ref, rtol=2e-6, atol=1e-6)

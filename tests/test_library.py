@@ -1,0 +1,70 @@
+"""CPU tests of the native boundary: libbonsai_p40.so loads, exports every
+symbol include/bonsai_p40.h declares, and the argument checks that run before
+any device work return the reference's codes (1 = invalid, 0 = no-op)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+import bonsai_p40 as B
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    text = open(os.path.join(ROOT, "include", "bonsai_p40.h")).read()
+    return sorted(set(re.findall(r"^int\s+(bonsai_p40_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_header_symbol():
+    L = B.lib()
+    syms = header_symbols()
+    assert len(syms) >= 13
+    for s in syms:
+        assert hasattr(L, s), s
+    assert set(syms) == set(B.SIGNATURES)
+
+
+def test_reference_symbol_set_is_kept():
+    ref = ["bonsai_p40_gemv", "bonsai_p40_quant_activations", "bonsai_p40_gemm",
+           "bonsai_p40_repack", "bonsai_p40_gemv_repack", "bonsai_p40_fwht",
+           "bonsai_p40_rmsnorm", "bonsai_p40_gdn_step", "bonsai_p40_attn"]
+    assert set(ref) <= set(header_symbols())
+
+
+NULL = None
+
+
+@pytest.mark.parametrize("name,args,rc", [
+    ("bonsai_p40_gemv", (NULL, NULL, NULL, 16, 100), 1),        # n_in % 128
+    ("bonsai_p40_gemv", (NULL, NULL, NULL, 16, 0), 1),          # n_in <= 0
+    ("bonsai_p40_gemv", (NULL, NULL, NULL, 0, 128), 0),         # empty no-op
+    ("bonsai_p40_gemv", (NULL, 2, NULL, 16, 128), 1),           # misaligned xq
+    ("bonsai_p40_chunk_dots", (NULL, NULL, NULL, 16, 96), 1),
+    ("bonsai_p40_quant_activations", (NULL, NULL, 33), 1),
+    ("bonsai_p40_quant_activations", (NULL, NULL, 0), 1),
+    ("bonsai_p40_gemm", (NULL, NULL, NULL, 16, 96, 4), 1),
+    ("bonsai_p40_gemm", (NULL, NULL, NULL, 0, 128, 4), 0),
+    ("bonsai_p40_gemm", (NULL, NULL, NULL, 16, 128, 0), 0),
+    ("bonsai_p40_repack", (NULL, NULL, 4, 128 * 12), 1),        # nb % 8
+    ("bonsai_p40_repack", (NULL, NULL, 0, 1024), 1),
+    ("bonsai_p40_gemv_repack", (NULL, NULL, NULL, 4, 128 * 4), 1),
+    ("bonsai_p40_fwht", (NULL, NULL, 1000), 1),
+    ("bonsai_p40_fwht", (NULL, NULL, 0), 1),
+    ("bonsai_p40_fwht_quant", (NULL, NULL, NULL, 512), 1),
+    ("bonsai_p40_quant_tokens", (NULL, NULL, NULL, 1000, 2, 1), 1),
+    ("bonsai_p40_quant_tokens", (NULL, NULL, NULL, 1024, 0, 1), 1),
+    ("bonsai_p40_swiglu_fwht_quant", (NULL, NULL, NULL, NULL, 100), 1),
+    ("bonsai_p40_rmsnorm", (NULL, NULL, NULL, 0, 64, C.c_float(1e-6)), 0),
+    ("bonsai_p40_rmsnorm", (NULL, NULL, NULL, 4, 0, C.c_float(1e-6)), 1),
+])
+def test_argument_checks(name, args, rc):
+    fn = getattr(B.lib(), name)
+    assert fn(*args, None) == rc
+
+
+def test_out_of_scope_entries_report_not_implemented():
+    L = B.lib()
+    assert L.bonsai_p40_gdn_step(*([None] * 7), 16, 48, 128, 128, None) == 2
+    assert L.bonsai_p40_attn(*([None] * 4), 4, 24, 4, 256, C.c_float(0.0625), None) == 2
