@@ -105,6 +105,19 @@ def bench_gemv(n_out, n_in, steps, warmup, gen, n_tok=1):
     return ms
 
 
+def bench_stream_read(nbytes, steps, warmup, blocks=8192):
+    """Achievable-read ceiling at the GEMV's byte count: bonsai_p40_stream_read
+    over rotating buffers of the same size (the analog of tools/bwtest.cu)."""
+    nbytes = (nbytes + 255) // 256 * 256
+    R = copies_for(nbytes)
+    buf = torch.empty(R * nbytes, dtype=torch.uint8, device="cuda")
+    out = torch.zeros(blocks, dtype=torch.int32, device="cuda")
+    base = buf.data_ptr()
+    ms = time_loop(lambda i: B.stream_read(base + (i % R) * nbytes, nbytes, out, blocks), steps, warmup)
+    del buf
+    return ms
+
+
 def bench_prepass(n, steps, warmup, gen):
     x = torch.randn(n, generator=gen, device="cuda")
     q = torch.empty(B.q8_bytes(n), dtype=torch.uint8, device="cuda")
@@ -212,6 +225,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--only-gemv", action="store_true", help="headline GEMV loop only (profiling)")
+    ap.add_argument("--only-read", action="store_true",
+                    help="stream-read probe over 23,750,272-byte buffers only (PMC calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -224,6 +239,11 @@ def main():
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
 
+    if args.only_read:
+        ms = bench_stream_read(gemv_bytes(N_FF, N_EMBD), args.steps, args.warmup)
+        print(f"[bench] stream_read 23750272 B: {ms * 1e3:.2f} us", file=sys.stderr, flush=True)
+        return
+
     # ---- headline: decode GEMV 17408x5120
     ms = bench_gemv(N_FF, N_EMBD, args.steps, args.warmup, gen)
     nbytes = gemv_bytes(N_FF, N_EMBD)
@@ -233,6 +253,12 @@ def main():
         return
 
     extra = {}
+    ms_read = bench_stream_read(nbytes, args.steps, args.warmup)
+    read_gbs = nbytes / (ms_read * 1e-3) / 1e9
+    extra["stream_read_same_bytes"] = {"us": round(ms_read * 1e3, 3), "GB/s": round(read_gbs, 1),
+                                       "note": "plain 16-byte streaming read of 23,750,272 B per launch: "
+                                               "the achievable ceiling for one launch of this size"}
+    print(f"[bench] stream read ceiling: {extra['stream_read_same_bytes']}", file=sys.stderr, flush=True)
     if not args.quick:
         for (n_out, n_in, tag) in ((N_EMBD, N_FF, "gemv_5120x17408"), (N_EMBD, N_EMBD, "gemv_5120x5120")):
             m = bench_gemv(n_out, n_in, args.steps, args.warmup, gen)
@@ -265,9 +291,10 @@ def main():
                       file=sys.stderr, flush=True)
 
     traffic = load_traffic(os.path.join(ROOT, "profiles", "gemv_17408x5120_traffic.json"))
-    roof = {"bound": "hbm", "kernel": "gemv_stream_kernel (bonsai_p40_gemv)",
+    roof = {"bound": "hbm", "kernel": "gemv_nb_kernel<40> (bonsai_p40_gemv)",
             "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "frac_of_achievable": round(gbs / read_gbs, 4),
             "traffic": traffic.get("bytes_per_launch") if traffic else None,
             "algorithmic_bytes": nbytes}
     cpu = None

@@ -123,6 +123,14 @@ int bonsai_p40_swiglu_fwht_quant(const float * gate, const float * up, const flo
 int bonsai_p40_chunk_dots(const void * W, const void * xq, int32_t * out,
                           int64_t n_out, int64_t n_in, bonsai_stream stream);
 
+// Measurement helper: a streaming read of `bytes` (16-byte aligned, multiple
+// of 16) with `blocks` workgroups of 256 lanes -- the achievable-HBM-bandwidth
+// ceiling the GEMV is compared with (the role of the reference's
+// tools/bwtest.cu).  `out` needs `blocks` words; it is written only in a
+// practically impossible case.  Errors: 1 on bad sizes or alignment.
+int bonsai_p40_stream_read(const void * buf, int64_t bytes, uint32_t * out, int blocks,
+                           bonsai_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -40,6 +40,7 @@ SIGNATURES = {
     "bonsai_p40_quant_tokens": [_F32P, _F32P, _V, _I64, _I64, C.c_int, _V],
     "bonsai_p40_swiglu_fwht_quant": [_F32P, _F32P, _F32P, _V, _I64, _V],
     "bonsai_p40_chunk_dots": [_V, _V, _V, _I64, _I64, _V],
+    "bonsai_p40_stream_read": [_V, _I64, _V, C.c_int, _V],
 }
 
 _lib = None
@@ -142,6 +143,11 @@ def swiglu_fwht_quant(gate, up, signs, xq, n: int, stream=None) -> None:
 def chunk_dots(W, xq, out, n_out: int, n_in: int, stream=None) -> None:
     _check("bonsai_p40_chunk_dots",
            call("bonsai_p40_chunk_dots", W, xq, out, n_out, n_in, stream=stream))
+
+
+def stream_read(buf, nbytes: int, out, blocks: int, stream=None) -> None:
+    _check("bonsai_p40_stream_read",
+           call("bonsai_p40_stream_read", buf, nbytes, out, blocks, stream=stream))
 
 
 # --------------------------------------------------------- sizes / helpers

@@ -172,6 +172,177 @@ gemv_stream_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Shape-specialised streaming kernel (compile-time nb for the model's row
+// widths).  Same unit/slot walk as gemv_stream_kernel, but
+//   * one wave per workgroup, no workgroup barrier: each lane loads the Q8_1
+//     blocks of exactly the chunks it multiplies into registers, once, and
+//     keeps them for every unit (a unit's slot j always meets the same
+//     activation chunk, (64j + lane) mod 4nb);
+//   * the first unit's weight loads are issued before the activation loads;
+//   * the slot loop is fully unrolled, so every LDS offset is an immediate
+//     and the row of each slot is known at compile time;
+//   * the chunk dot is the 16x-scaled form (one shift per code word), the
+//   scale 1/16 folded into the activation scale.
+// G = 1 when 4*nb % 64 == 0; otherwise G = 2 if that needs <= 8 slots, else
+// G = 1 with a half-empty last slot whose idle lanes carry zero activations.
+template <int NB>
+struct NbSpec {
+    static constexpr int NCH = 4 * NB;
+    static constexpr int G = (NCH % 64 == 0) ? 1 : ((2 * NCH / 64) <= 8 ? 2 : 1);
+    static constexpr int S = (G * NCH + 63) / 64;
+    static constexpr int UB = G * PQ2_BYTES * NB;
+    static constexpr int NPIECE = UB / 16;
+    static constexpr int NPL = (NPIECE + 63) / 64;
+    // LDS bytes per unit buffer: the slot windows (S * 544 + 16) and every
+    // byte a full NPL-instruction DMA can write (1024 * NPL)
+    static constexpr int LDSB = (S * SLOT_BYTES + 16 > 1024 * NPL) ? S * SLOT_BYTES + 16 : 1024 * NPL;
+    static constexpr int SPLIT = (G == 2) ? NCH / 64 : -1;
+    static constexpr bool PARTIAL = (G * NCH) % 64 != 0;   // last slot has idle lanes 32..63
+};
+
+typedef int v4i_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+// s_waitcnt vmcnt(N) with the other counters left open (gfx9 encoding:
+// vmcnt[3:0] at bits 3:0, vmcnt[5:4] at 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int NB, int D, bool DUMP>
+__global__ void __launch_bounds__(64)
+gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
+               float * __restrict__ y, int32_t * __restrict__ dump, int n_out, int units_per_wave) {
+    using P = NbSpec<NB>;
+    static_assert(D >= 1 && D <= 4, "ring depth");
+    static_assert((D - 1) * P::NPL < 64, "vmcnt range");
+    __shared__ __attribute__((aligned(16))) uint8_t ring[D][P::LDSB];
+    const int lane = threadIdx.x;
+    const int n_units = (n_out + P::G - 1) / P::G;
+    const int u0 = blockIdx.x * units_per_wave;
+    const int nu = min(units_per_wave, n_units - u0);
+    const size_t total_bytes = (size_t)n_out * PQ2_BYTES * NB;
+
+    // 1. activation chunks of this lane, one per slot (plain loads, first)
+    int act[P::S][8];
+    uint32_t dsw[P::S];
+#pragma unroll
+    for (int j = 0; j < P::S; ++j) {
+        const int v = 64 * j + lane;
+        int c = v >= P::NCH ? v - P::NCH : v;
+        c = v < P::G * P::NCH ? c : 0;
+        const uint8_t * blk = xq + (size_t)Q81_BYTES * c;
+        dsw[j] = *reinterpret_cast<const uint32_t *>(blk);
+        const v4i_a4 q0 = *reinterpret_cast<const v4i_a4 *>(blk + 4);
+        const v4i_a4 q1 = *reinterpret_cast<const v4i_a4 *>(blk + 20);
+        act[j][0] = q0.x; act[j][1] = q0.y; act[j][2] = q0.z; act[j][3] = q0.w;
+        act[j][4] = q1.x; act[j][5] = q1.y; act[j][6] = q1.z; act[j][7] = q1.w;
+    }
+
+    // 2. weight units stream straight into LDS (global_load_lds_dwordx4: 64
+    //    lanes x 16 B land contiguously at the wave-uniform LDS base).  Every
+    //    unit is exactly NPL instructions, so "unit i has landed" is
+    //    vmcnt <= NPL * (units issued after i).
+    //    The DMA is issued without exec masking so the compiler can count
+    //    it: lanes past the unit (or past the end of W in a half-filled last
+    //    unit) re-read the unit's last in-bounds piece; what they land in LDS
+    //    lies beyond the unit bytes or belongs to a row that is never stored.
+    const size_t last_piece = total_bytes / 16 - 1;
+    auto issue = [&](int uu, int slot) {
+        const size_t base = (size_t)uu * (P::UB / 16);
+#pragma unroll
+        for (int k = 0; k < P::NPL; ++k) {
+            size_t p = base + (size_t)min(lane + 64 * k, P::NPIECE - 1);
+            p = p < last_piece ? p : last_piece;
+            __builtin_amdgcn_global_load_lds(W + 16 * p, (lds_void *)(&ring[slot][1024 * k]), 16, 0, 0);
+        }
+    };
+    __builtin_amdgcn_sched_barrier(0);        // keep the activation loads ahead of the DMA
+#pragma unroll
+    for (int i = 0; i < D; ++i) issue(u0 + min(i, nu - 1), i);
+    __builtin_amdgcn_sched_barrier(0);
+
+    float da16[P::S];
+    int bias16[P::S];
+#pragma unroll
+    for (int j = 0; j < P::S; ++j) {
+        const bool valid = 64 * j + lane < P::G * P::NCH;
+        da16[j] = valid ? f16_bits_to_f32(dsw[j] & 0xffffu) * (1.0f / 16.0f) : 0.0f;
+        bias16[j] = valid ? -16 * (int)(int16_t)(dsw[j] >> 16) : 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) act[j][k] = valid ? act[j][k] : 0;
+    }
+
+    const int cw = PQ2_BYTES * (lane >> 2) + 2 + 8 * (lane & 3);
+    const int sh = cw & 3;
+    const int cw_al = cw - sh;
+    const int dwo = PQ2_BYTES * (lane >> 2);
+    float ykeep = 0.0f;                       // lane j keeps the output of row u0*G + j
+
+    int i = 0;
+    do {                                      // nu >= 1: the launcher sizes the grid exactly
+        const int slot = i % D;
+        const int newer = min(D - 1, nu - 1 - i);
+        if (newer >= 3) wait_vmcnt<3 * P::NPL>();
+        else if (newer == 2) wait_vmcnt<2 * P::NPL>();
+        else if (newer == 1) wait_vmcnt<P::NPL>();
+        else wait_vmcnt<0>();
+        __builtin_amdgcn_wave_barrier();
+        const uint8_t * ub = ring[slot];
+        const int u = u0 + i;
+
+        float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < P::S; ++j) {
+            const uint8_t * cp = ub + cw_al + SLOT_BYTES * j;
+            const uint32_t d0 = *reinterpret_cast<const uint32_t *>(cp);
+            const uint32_t d1 = *reinterpret_cast<const uint32_t *>(cp + 4);
+            const uint32_t d2 = *reinterpret_cast<const uint32_t *>(cp + 8);
+            const uint32_t w0 = __builtin_amdgcn_alignbyte(d1, d0, sh);
+            const uint32_t w1 = __builtin_amdgcn_alignbyte(d2, d1, sh);
+            const uint32_t dwb = *reinterpret_cast<const uint16_t *>(ub + dwo + SLOT_BYTES * j);
+            const int s16 = chunk_dot_x16(w0, w1, act[j], bias16[j]);
+            const bool second = (P::G == 2) && (j > P::SPLIT || (j == P::SPLIT && lane >= 32));
+            if (DUMP) {
+                const int v = 64 * j + lane;
+                const int row = u * P::G + (second ? 1 : 0);
+                if (v < P::G * P::NCH && row < n_out)
+                    dump[(size_t)row * P::NCH + (second ? v - P::NCH : v)] = s16 >> 4;
+            } else {
+                const float t = da16[j] * (float)s16;
+                float dw = f16_bits_to_f32(dwb);
+                if (P::PARTIAL && j == P::S - 1) dw = lane < 32 ? dw : 0.0f;   // idle lanes: LDS past the unit
+                if (P::G == 1 || j < P::SPLIT) acc0 = fmaf(dw, t, acc0);
+                else if (j > P::SPLIT) acc1 = fmaf(dw, t, acc1);
+                else if (lane < 32) acc0 = fmaf(dw, t, acc0);
+                else acc1 = fmaf(dw, t, acc1);
+            }
+        }
+        if (!DUMP) {
+            const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_to_lane63(acc0)), 63));
+            ykeep = (lane == P::G * i) ? t0 : ykeep;
+            if (P::G == 2) {
+                const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_to_lane63(acc1)), 63));
+                ykeep = (lane == P::G * i + 1) ? t1 : ykeep;
+            }
+        }
+        // refill this slot with unit i + D once every lane's reads returned
+        if (i + D < nu) {
+            __builtin_amdgcn_s_waitcnt(0xC07F);    // lgkmcnt(0)
+            __builtin_amdgcn_wave_barrier();
+            issue(u0 + i + D, slot);
+        }
+    } while (++i < nu);
+    if (!DUMP) {
+        const int row = u0 * P::G + lane;
+        if (lane < nu * P::G && row < n_out) y[row] = ykeep;
+    }
+}
+
 // Generic path: one wave per row, lane-strided chunks, 2-byte weight loads
 // (any n_in % 128 == 0, any 2-byte aligned W).
 template <bool DUMP>
@@ -263,16 +434,51 @@ int launch_stream_g(const uint8_t * W, const uint8_t * xq, float * y, int32_t * 
     }
 }
 
+template <int NB, bool DUMP>
+int launch_nb(const uint8_t * W, const uint8_t * xq, float * y, int32_t * dump, int n_out,
+              hipStream_t st) {
+    using P = NbSpec<NB>;
+    const int n_units = (n_out + P::G - 1) / P::G;
+    int upw = env_int("BONSAI_GEMV_UNITS_PER_WAVE", 0);
+    if (upw <= 0) {
+        const int target_waves = 256 * 12;
+        upw = (n_units + target_waves - 1) / target_waves;
+    }
+    upw = upw < 1 ? 1 : (upw > 64 / P::G ? 64 / P::G : upw);
+    const int waves = (n_units + upw - 1) / upw;
+    // ring depth: all of a wave's units in flight when it owns <= 3
+    if (upw == 1)
+        hipLaunchKernelGGL((gemv_nb_kernel<NB, 1, DUMP>), dim3(waves), dim3(64), 0, st, W, xq, y, dump, n_out, upw);
+    else if (upw == 2)
+        hipLaunchKernelGGL((gemv_nb_kernel<NB, 2, DUMP>), dim3(waves), dim3(64), 0, st, W, xq, y, dump, n_out, upw);
+    else
+        hipLaunchKernelGGL((gemv_nb_kernel<NB, 3, DUMP>), dim3(waves), dim3(64), 0, st, W, xq, y, dump, n_out, upw);
+    return (int)hipGetLastError();
+}
+
 template <bool DUMP>
 int gemv_dispatch(const void * W, const void * xq, float * y, int32_t * dump, int64_t n_out,
                   int64_t n_in, hipStream_t st) {
     const uint8_t * w = static_cast<const uint8_t *>(W);
     const uint8_t * x = static_cast<const uint8_t *>(xq);
     if (n_out > 0x7fffffff || n_in / QK_PQ2 > (1 << 24)) return 1;
+    const bool w_al16 = ((uintptr_t)w & 15u) == 0;
+    const int kernel_sel = env_int("BONSAI_GEMV_KERNEL", 0);   // 0 auto, 1 stream, 2 generic
+    if (w_al16 && kernel_sel == 0) {
+        switch (n_in / QK_PQ2) {
+            case 8: return launch_nb<8, DUMP>(w, x, y, dump, (int)n_out, st);
+            case 40: return launch_nb<40, DUMP>(w, x, y, dump, (int)n_out, st);
+            case 48: return launch_nb<48, DUMP>(w, x, y, dump, (int)n_out, st);
+            case 80: return launch_nb<80, DUMP>(w, x, y, dump, (int)n_out, st);
+            case 96: return launch_nb<96, DUMP>(w, x, y, dump, (int)n_out, st);
+            case 136: return launch_nb<136, DUMP>(w, x, y, dump, (int)n_out, st);
+            default: break;
+        }
+    }
     const StreamGeom g = stream_geom(n_in);
     const bool fast = (n_in % HBLK == 0) && (((uintptr_t)w & 15u) == 0) && g.npl <= MAX_NPL &&
                       g.lds_bytes <= (size_t)max_lds_per_block() &&
-                      env_int("BONSAI_GEMV_GENERIC", 0) == 0;
+                      kernel_sel != 2;
     if (fast) {
         const int rc = (g.G == 1) ? launch_stream_g<1, DUMP>(w, x, y, dump, (int)n_out, g, st)
                                   : launch_stream_g<2, DUMP>(w, x, y, dump, (int)n_out, g, st);

@@ -100,6 +100,28 @@ __device__ __forceinline__ int chunk_dot_i32(uint32_t w0, uint32_t w1, const int
     return s;
 }
 
+// Same chunk dot, scaled by 16 and with one extraction shift per word: bit
+// pairs 0 and 1 of every code byte are taken with the mask 0x03030303 from w
+// and w >> 2 (weight 1), bit pairs 2 and 3 with 0x30303030 from w and w >> 2,
+// which leaves 16 * code in each byte (<= 48, still a positive int8).  The two
+// partial sums combine as 16 * s1 + s16 with one v_lshl_add; `bias16` is
+// -16 * s.  The result is exactly 16 * sumi.
+__device__ __forceinline__ int chunk_dot_x16(uint32_t w0, uint32_t w1, const int (&a)[8],
+                                             int bias16) {
+    constexpr uint32_t M = 0x03030303u, M4 = 0x30303030u;
+    const uint32_t v0 = w0 >> 2, v1 = w1 >> 2;
+    int s1 = 0, s16 = bias16;
+    s1 = __builtin_amdgcn_sdot4((int)(w0 & M), a[0], s1, false);
+    s1 = __builtin_amdgcn_sdot4((int)(v0 & M), a[1], s1, false);
+    s16 = __builtin_amdgcn_sdot4((int)(w0 & M4), a[2], s16, false);
+    s16 = __builtin_amdgcn_sdot4((int)(v0 & M4), a[3], s16, false);
+    s1 = __builtin_amdgcn_sdot4((int)(w1 & M), a[4], s1, false);
+    s1 = __builtin_amdgcn_sdot4((int)(v1 & M), a[5], s1, false);
+    s16 = __builtin_amdgcn_sdot4((int)(w1 & M4), a[6], s16, false);
+    s16 = __builtin_amdgcn_sdot4((int)(v1 & M4), a[7], s16, false);
+    return (s1 << 4) + s16;
+}
+
 __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace pq2

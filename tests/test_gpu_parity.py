@@ -319,15 +319,26 @@ def test_ffn_chain_config1():
     B.swiglu_fwht_quant(g, u, None, hq, n_ff)
     y = torch.zeros(n_embd, dtype=torch.float32, device="cuda")
     B.gemv(dev(Wd), hq, y, n_embd, n_ff)
-    # oracle chain
+    # oracle chain, stage by stage: each GPU stage is compared with the oracle
+    # applied to the GPU's own input of that stage
     xq_o = O.quantize_q8_1(O.fwht(x), True)
     assert np.array_equal(host(xq), xq_o)
-    g_o = O.gemv(Wg, xq_o, n_ff, n_embd, 16)
-    u_o = O.gemv(Wu, xq_o, n_ff, n_embd, 16)
-    assert normwise(host(g), g_o) <= TOL and normwise(host(u), u_o) <= TOL
-    hq_o = O.quantize_q8_1(O.fwht(O.swiglu(g_o, u_o)), True)
-    y_o = O.gemv(Wd, hq_o, n_embd, n_ff, 16)
-    assert normwise(host(y), y_o) <= 1e-4
+    g_h, u_h = host(g), host(u)
+    assert normwise(g_h, O.gemv(Wg, xq_o, n_ff, n_embd, 16)) <= TOL
+    assert normwise(u_h, O.gemv(Wu, xq_o, n_ff, n_embd, 16)) <= TOL
+    hq_h = host(hq)
+    hq_o = O.quantize_q8_1(O.fwht(O.swiglu(g_h, u_h)), True)
+    _, _, q1 = O.q81_fields(hq_h)
+    _, _, q2 = O.q81_fields(hq_o)
+    assert np.max(np.abs(q1.astype(int) - q2.astype(int))) <= 1     # device vs glibc expf ulps
+    assert np.mean(q1 != q2) < 1e-3
+    assert normwise(host(y), O.gemv(Wd, hq_h, n_embd, n_ff, 16)) <= TOL
+    # end to end against the all-oracle chain: the Q8_1 re-quantisation of h
+    # turns 1e-6 differences in g, u into occasional +-1 steps of q, so the
+    # bound here is the quantisation noise level, not the fp32 tolerance
+    hq_full = O.quantize_q8_1(O.fwht(O.swiglu(O.gemv(Wg, xq_o, n_ff, n_embd, 16),
+                                                O.gemv(Wu, xq_o, n_ff, n_embd, 16))), True)
+    assert normwise(host(y), O.gemv(Wd, hq_full, n_embd, n_ff, 16)) <= 2e-3
 
 
 # ----------------------------------------------------------------- rmsnorm
