@@ -72,8 +72,9 @@ def synth_activation_q8(n_in: int, gen: torch.Generator, n_tok: int = 1) -> torc
 
 
 # --------------------------------------------------------------- timing
-def time_loop(fn, steps: int, warmup: int) -> float:
-    """ms per call of fn(i), HIP events on the current stream."""
+def time_loop_eager(fn, steps: int, warmup: int) -> float:
+    """ms per call of fn(i) launched one by one from Python (HIP events on
+    the current stream): includes the host launch cost of each call."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -84,6 +85,39 @@ def time_loop(fn, steps: int, warmup: int) -> float:
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+GRAPH = True
+
+
+def time_loop(fn, steps: int, warmup: int, per_graph: int = 0) -> float:
+    """ms per call of fn(i), measured on the GPU: `per_graph` consecutive
+    calls are captured once into a HIP graph, the graph is replayed until
+    `steps` calls ran, bracketed by HIP events on the stream the kernels run
+    on.  The graph only removes the host's per-call launch cost; every call is
+    still one full kernel launch (or more) on the stream."""
+    if not GRAPH:
+        return time_loop_eager(fn, steps, warmup)
+    k = per_graph or min(steps, 100)
+    reps = max(1, (steps + k - 1) // k)
+    for i in range(min(warmup, 3)):
+        fn(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(k):
+            fn(i)
+    for _ in range(max(1, warmup // k)):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del g
+    return e0.elapsed_time(e1) / (reps * k)
 
 
 def copies_for(nbytes: int, target: float = 1.1e9) -> int:
@@ -171,7 +205,7 @@ def bench_token_sweep(steps, warmup, gen):
                 B.fwht_quant(xs[n_in], None, qs[n_in], n_in)
                 B.gemv(W, qs[n_in], ys[n_out], n_out, n_in)
 
-    ms = time_loop(token, steps, warmup)
+    ms = time_loop(token, steps, warmup, per_graph=1)
     del layers, proto
     return ms, wbytes
 
@@ -225,6 +259,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--only-gemv", action="store_true", help="headline GEMV loop only (profiling)")
+    ap.add_argument("--eager", action="store_true",
+                    help="time Python launches one by one instead of replaying HIP graphs")
     ap.add_argument("--only-read", action="store_true",
                     help="stream-read probe over 23,750,272-byte buffers only (PMC calibration)")
     args = ap.parse_args()
@@ -236,12 +272,18 @@ def main():
         print("no GPU visible", file=sys.stderr)
         sys.exit(1)
     B.lib()
+    global GRAPH
+    GRAPH = not args.eager
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
 
     if args.only_read:
         ms = bench_stream_read(gemv_bytes(N_FF, N_EMBD), args.steps, args.warmup)
         print(f"[bench] stream_read 23750272 B: {ms * 1e3:.2f} us", file=sys.stderr, flush=True)
+        z = torch.empty(23750400 // 4, dtype=torch.float32, device="cuda")
+        for _ in range(args.steps):
+            z.zero_()              # writes 23,750,400 B: WRITE_SIZE calibration
+        torch.cuda.synchronize()
         return
 
     # ---- headline: decode GEMV 17408x5120
@@ -252,7 +294,17 @@ def main():
     if args.only_gemv:
         return
 
-    extra = {}
+    extra = {"timing": "HIP graph replay of back-to-back launches" if GRAPH else "eager Python launches"}
+    if GRAPH:
+        W0 = synth_weights(N_FF, N_EMBD, gen)
+        Rc = copies_for(W0.numel())
+        Ws = [W0] + [W0.clone() for _ in range(Rc - 1)]
+        xq = synth_activation_q8(N_EMBD, gen)
+        yv = torch.empty(N_FF, device="cuda")
+        me = time_loop_eager(lambda i: B.gemv(Ws[i % Rc], xq, yv, N_FF, N_EMBD), args.steps, args.warmup)
+        extra["gemv_17408x5120_eager_python_launch"] = {"us": round(me * 1e3, 3),
+                                                        "GB/s": round(nbytes / (me * 1e-3) / 1e9, 1)}
+        del Ws, W0
     ms_read = bench_stream_read(nbytes, args.steps, args.warmup)
     read_gbs = nbytes / (ms_read * 1e-3) / 1e9
     extra["stream_read_same_bytes"] = {"us": round(ms_read * 1e3, 3), "GB/s": round(read_gbs, 1),

@@ -213,44 +213,56 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <int NB, int D, bool DUMP>
-__global__ void __launch_bounds__(64)
+// Reduce acc0 over lanes 0..63 and acc1 over lanes 0..63 at once:
+// v_permlane32_swap folds the upper half of acc0 onto its lower half and the
+// lower half of acc1 onto its upper half in one exchange, then one DPP tree
+// sums each 32-lane half.  Row totals land in lanes 31 (acc0) and 63 (acc1).
+__device__ __forceinline__ float wave_sum2_to_lanes31_63(float acc0, float acc1) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(acc0), __float_as_int(acc1), false, false);
+    float v = __int_as_float(sw[0]) + __int_as_float(sw[1]);
+    v += dpp_mov<DPP_QUAD_XOR1>(v);
+    v += dpp_mov<DPP_QUAD_XOR2>(v);
+    v += dpp_mov<DPP_ROW_HALF_MIRROR>(v);
+    v += dpp_mov<DPP_ROW_MIRROR>(v);
+    v += dpp_mov<DPP_ROW_BCAST15, 0xa>(v);
+    return v;
+}
+
+// Workgroup of WAVES waves.  Each wave owns `units_per_wave` consecutive
+// units and a private ring of D unit buffers in LDS; the workgroup shares one
+// LDS copy of the Q8_1 activation.  Every global read is an LDS DMA
+// (global_load_lds_dwordx4), so the only waits are the explicit vmcnt waits
+// below, and each unit is consumed as soon as its own bytes have landed.
+template <int NB, int D, int WAVES, bool DUMP>
+__global__ void __launch_bounds__(64 * WAVES)
 gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
                float * __restrict__ y, int32_t * __restrict__ dump, int n_out, int units_per_wave) {
     using P = NbSpec<NB>;
-    static_assert(D >= 1 && D <= 4, "ring depth");
-    static_assert((D - 1) * P::NPL < 64, "vmcnt range");
-    __shared__ __attribute__((aligned(16))) uint8_t ring[D][P::LDSB];
-    const int lane = threadIdx.x;
+    static_assert(D >= 1 && D <= 3, "ring depth");
+    static_assert(D * P::NPL < 64, "vmcnt range");
+    constexpr int ACT_BYTES = Q81_BYTES * P::NCH;
+    constexpr int NA = (ACT_BYTES + 1023) / 1024;          // activation DMA instructions
+    __shared__ __attribute__((aligned(16))) uint8_t act_lds[NA * 1024];
+    __shared__ __attribute__((aligned(16))) uint8_t ring_all[WAVES][D][P::LDSB];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    __builtin_assume(lane >= 0 && lane < 64);
+    uint8_t (*ring)[P::LDSB] = ring_all[wave];
     const int n_units = (n_out + P::G - 1) / P::G;
-    const int u0 = blockIdx.x * units_per_wave;
-    const int nu = min(units_per_wave, n_units - u0);
+    const int u0 = (blockIdx.x * WAVES + wave) * units_per_wave;
+    const int nu = min(units_per_wave, n_units - u0);       // <= 0 for idle trailing waves
     const size_t total_bytes = (size_t)n_out * PQ2_BYTES * NB;
 
-    // 1. activation chunks of this lane, one per slot (plain loads, first)
-    int act[P::S][8];
-    uint32_t dsw[P::S];
-#pragma unroll
-    for (int j = 0; j < P::S; ++j) {
-        const int v = 64 * j + lane;
-        int c = v >= P::NCH ? v - P::NCH : v;
-        c = v < P::G * P::NCH ? c : 0;
-        const uint8_t * blk = xq + (size_t)Q81_BYTES * c;
-        dsw[j] = *reinterpret_cast<const uint32_t *>(blk);
-        const v4i_a4 q0 = *reinterpret_cast<const v4i_a4 *>(blk + 4);
-        const v4i_a4 q1 = *reinterpret_cast<const v4i_a4 *>(blk + 20);
-        act[j][0] = q0.x; act[j][1] = q0.y; act[j][2] = q0.z; act[j][3] = q0.w;
-        act[j][4] = q1.x; act[j][5] = q1.y; act[j][6] = q1.z; act[j][7] = q1.w;
+    // 1. activation share of this wave (instructions k = wave, wave + WAVES, ...)
+    for (int k = wave; k < NA; k += WAVES) {
+        const int off = min(16 * (64 * k + lane), ACT_BYTES - 16);
+        __builtin_amdgcn_global_load_lds(xq + off, (lds_void *)(&act_lds[1024 * k]), 16, 0, 0);
     }
+    __builtin_amdgcn_sched_barrier(0);
 
-    // 2. weight units stream straight into LDS (global_load_lds_dwordx4: 64
-    //    lanes x 16 B land contiguously at the wave-uniform LDS base).  Every
-    //    unit is exactly NPL instructions, so "unit i has landed" is
-    //    vmcnt <= NPL * (units issued after i).
-    //    The DMA is issued without exec masking so the compiler can count
-    //    it: lanes past the unit (or past the end of W in a half-filled last
-    //    unit) re-read the unit's last in-bounds piece; what they land in LDS
-    //    lies beyond the unit bytes or belongs to a row that is never stored.
+    // 2. the first D units (unit i exactly NPL instructions; lanes past the
+    //    unit or past W re-read the last in-bounds piece, landing in LDS past
+    //    the unit bytes or in a row that is never stored)
     const size_t last_piece = total_bytes / 16 - 1;
     auto issue = [&](int uu, int slot) {
         const size_t base = (size_t)uu * (P::UB / 16);
@@ -261,20 +273,34 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
             __builtin_amdgcn_global_load_lds(W + 16 * p, (lds_void *)(&ring[slot][1024 * k]), 16, 0, 0);
         }
     };
-    __builtin_amdgcn_sched_barrier(0);        // keep the activation loads ahead of the DMA
+    if (nu > 0) {
 #pragma unroll
-    for (int i = 0; i < D; ++i) issue(u0 + min(i, nu - 1), i);
+        for (int i = 0; i < D; ++i) issue(u0 + min(i, nu - 1), i);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
+    // 3. own activation share landed (all unit DMAs are younger), then the
+    //    workgroup barrier makes every share visible
+    if (nu > 0) wait_vmcnt<D * P::NPL>();
+    else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    if (nu <= 0) return;
+
+    int act[P::S][8];
     float da16[P::S];
     int bias16[P::S];
 #pragma unroll
     for (int j = 0; j < P::S; ++j) {
-        const bool valid = 64 * j + lane < P::G * P::NCH;
-        da16[j] = valid ? f16_bits_to_f32(dsw[j] & 0xffffu) * (1.0f / 16.0f) : 0.0f;
-        bias16[j] = valid ? -16 * (int)(int16_t)(dsw[j] >> 16) : 0;
+        const int v = 64 * j + lane;
+        const bool valid = v < P::G * P::NCH;
+        int c = v >= P::NCH ? v - P::NCH : v;
+        c = valid ? c : 0;
+        const uint32_t * a = reinterpret_cast<const uint32_t *>(&act_lds[Q81_BYTES * c]);
+        const uint32_t ds = a[0];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) act[j][k] = valid ? act[j][k] : 0;
+        for (int k = 0; k < 8; ++k) act[j][k] = valid ? (int)a[1 + k] : 0;
+        da16[j] = valid ? f16_bits_to_f32(ds & 0xffffu) * (1.0f / 16.0f) : 0.0f;
+        bias16[j] = valid ? -16 * (int)(int16_t)(ds >> 16) : 0;
     }
 
     const int cw = PQ2_BYTES * (lane >> 2) + 2 + 8 * (lane & 3);
@@ -284,11 +310,10 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
     float ykeep = 0.0f;                       // lane j keeps the output of row u0*G + j
 
     int i = 0;
-    do {                                      // nu >= 1: the launcher sizes the grid exactly
+    do {
         const int slot = i % D;
         const int newer = min(D - 1, nu - 1 - i);
-        if (newer >= 3) wait_vmcnt<3 * P::NPL>();
-        else if (newer == 2) wait_vmcnt<2 * P::NPL>();
+        if (newer >= 2) wait_vmcnt<2 * P::NPL>();
         else if (newer == 1) wait_vmcnt<P::NPL>();
         else wait_vmcnt<0>();
         __builtin_amdgcn_wave_barrier();
@@ -323,11 +348,14 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
             }
         }
         if (!DUMP) {
-            const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_to_lane63(acc0)), 63));
-            ykeep = (lane == P::G * i) ? t0 : ykeep;
             if (P::G == 2) {
-                const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_to_lane63(acc1)), 63));
-                ykeep = (lane == P::G * i + 1) ? t1 : ykeep;
+                const float v = wave_sum2_to_lanes31_63(acc0, acc1);
+                const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+                const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+                ykeep = (lane == 2 * i) ? t0 : ((lane == 2 * i + 1) ? t1 : ykeep);
+            } else {
+                const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_to_lane63(acc0)), 63));
+                ykeep = (lane == i) ? t0 : ykeep;
             }
         }
         // refill this slot with unit i + D once every lane's reads returned
@@ -434,26 +462,47 @@ int launch_stream_g(const uint8_t * W, const uint8_t * xq, float * y, int32_t * 
     }
 }
 
-template <int NB, bool DUMP>
-int launch_nb(const uint8_t * W, const uint8_t * xq, float * y, int32_t * dump, int n_out,
-              hipStream_t st) {
+int cu_count() {
+    static int v = -1;
+    if (v < 0) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        int x = 0;
+        if (hipDeviceGetAttribute(&x, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || x <= 0)
+            x = 256;
+        v = x;
+    }
+    return v;
+}
+
+template <int NB, int D, int WAVES, bool DUMP>
+int launch_nb_t(const uint8_t * W, const uint8_t * xq, float * y, int32_t * dump, int n_out,
+                hipStream_t st) {
     using P = NbSpec<NB>;
+    constexpr size_t lds = (size_t)((Q81_BYTES * P::NCH + 1023) / 1024) * 1024 + (size_t)WAVES * D * P::LDSB;
     const int n_units = (n_out + P::G - 1) / P::G;
     int upw = env_int("BONSAI_GEMV_UNITS_PER_WAVE", 0);
     if (upw <= 0) {
-        const int target_waves = 256 * 12;
-        upw = (n_units + target_waves - 1) / target_waves;
+        // enough units per wave that every wave fits on the GPU at once
+        int wg_per_cu = (int)((160 * 1024) / lds);
+        wg_per_cu = wg_per_cu < 1 ? 1 : (wg_per_cu > 20 / WAVES ? 20 / WAVES : wg_per_cu);
+        const int resident = cu_count() * wg_per_cu * WAVES;
+        upw = (n_units + resident - 1) / resident;
     }
     upw = upw < 1 ? 1 : (upw > 64 / P::G ? 64 / P::G : upw);
     const int waves = (n_units + upw - 1) / upw;
-    // ring depth: all of a wave's units in flight when it owns <= 3
-    if (upw == 1)
-        hipLaunchKernelGGL((gemv_nb_kernel<NB, 1, DUMP>), dim3(waves), dim3(64), 0, st, W, xq, y, dump, n_out, upw);
-    else if (upw == 2)
-        hipLaunchKernelGGL((gemv_nb_kernel<NB, 2, DUMP>), dim3(waves), dim3(64), 0, st, W, xq, y, dump, n_out, upw);
-    else
-        hipLaunchKernelGGL((gemv_nb_kernel<NB, 3, DUMP>), dim3(waves), dim3(64), 0, st, W, xq, y, dump, n_out, upw);
+    const int blocks = (waves + WAVES - 1) / WAVES;
+    hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, DUMP>), dim3(blocks), dim3(64 * WAVES), 0, st, W, xq,
+                       y, dump, n_out, upw);
     return (int)hipGetLastError();
+}
+
+template <int NB, bool DUMP>
+int launch_nb(const uint8_t * W, const uint8_t * xq, float * y, int32_t * dump, int n_out,
+              hipStream_t st) {
+    // ring depth 2 for the widest rows keeps two 4-wave workgroups per CU
+    if (NB >= 96) return launch_nb_t<NB, 2, 4, DUMP>(W, xq, y, dump, n_out, st);
+    return launch_nb_t<NB, 3, 4, DUMP>(W, xq, y, dump, n_out, st);
 }
 
 template <bool DUMP>
@@ -464,7 +513,7 @@ int gemv_dispatch(const void * W, const void * xq, float * y, int32_t * dump, in
     if (n_out > 0x7fffffff || n_in / QK_PQ2 > (1 << 24)) return 1;
     const bool w_al16 = ((uintptr_t)w & 15u) == 0;
     const int kernel_sel = env_int("BONSAI_GEMV_KERNEL", 0);   // 0 auto, 1 stream, 2 generic
-    if (w_al16 && kernel_sel == 0) {
+    if (w_al16 && ((uintptr_t)x & 15u) == 0 && kernel_sel == 0) {
         switch (n_in / QK_PQ2) {
             case 8: return launch_nb<8, DUMP>(w, x, y, dump, (int)n_out, st);
             case 40: return launch_nb<40, DUMP>(w, x, y, dump, (int)n_out, st);
