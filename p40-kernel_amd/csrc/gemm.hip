@@ -5,20 +5,25 @@
 // with S the exact integer chunk dot sum (code-1)*q over the 32 weights of
 // chunk p of block b, and X chunk-major (block (c, t) at c*n_tok + t).
 //
-// Tile design: a workgroup of 4 waves computes a (32*WM) x (32*WN) tile of
-// (rows x tokens); each wave owns a 32 x 32 sub-tile.  Per PQ2_0 block
-// (K = 128 = 4 chunks) the workgroup stages the block's codes and fp16 d of
-// its rows and the 4 Q8_1 chunks of its tokens in LDS; each chunk is then one
-// v_mfma_i32_32x32x32_i8 per wave (K = 32 = one chunk, so the int32 result is
-// exactly S for every (row, token) of the sub-tile):
-//   * A (rows x 32): codes unpacked to int8 (code - 1) in registers with SWAR
-//     ((w >> 2k) & 0x03030303, then +0x7f7f7f7f ^ 0x80808080 per byte), so the
-//     "- s" bias of the reference is folded into the product;
-//   * B (32 x tokens): the permuted Q8_1 bytes as stored -- the code word
-//     extraction order k, k+4, k+8, k+12 matches the activation permutation,
-//     so A and B share the same K order without any shuffle;
-//   * epilogue per chunk: inner += da[t] * float(S) (per token scale), per
-//     block: acc += dw[r] * inner (per row scale) -- fp32, as the reference.
+// Design
+// ------
+// * One v_mfma_i32_32x32x32_i8 covers one Q8_1 chunk (K = 32) for a 32x32
+//   (rows x tokens) tile, so its int32 result is exactly S for every element.
+//   A = codes unpacked to int8 (code - 1) with SWAR ((w >> 2k) & 0x03030303,
+//   then +0x7f7f7f7f ^ 0x80808080 per byte), which folds the reference's "- s"
+//   bias into the product; B = the permuted Q8_1 bytes as stored: the code
+//   word extraction order k, k+4, k+8, k+12 is the activation permutation, so
+//   A and B share one K order without any shuffle.
+// * Epilogue per chunk: inner += da[t] * float(S) (per-token scale); per block
+//   acc += dw[r] * inner (per-row scale).  This fp32 rescale per (row, token,
+//   chunk) -- about 2.25 VALU instructions per element per chunk against one
+//   32-cycle MFMA per 1024 elements -- is what bounds the kernel.
+// * Workgroup tile BM x BN = 128 x 128 (8 waves, 4 x 2, each 32 x 64 = 1 x 2
+//   MFMA tiles sharing one unpacked A operand).  Per PQ2_0 block (K = 128) the workgroup stages the tile's
+//   codes (realigned to dwords), block scales and the 4 Q8_1 chunks of its
+//   tokens in LDS; the next block's global loads are issued into registers
+//   before the current block is computed.
+// * Small batches (n_tok <= 32) use a 128 x 32 tile (4 waves stacked on rows).
 #include "pq2_device.h"
 #include "../../include/bonsai_p40.h"
 
@@ -34,13 +39,26 @@ __device__ __forceinline__ int codes_minus_one(uint32_t w, int k) {
     return (int)((t + 0x7f7f7f7fu) ^ 0x80808080u);
 }
 
-template <int WM, int WN>
-__global__ void __launch_bounds__(256)
+// WM x WN waves, each owning TM x TN MFMA tiles of 32 x 32.
+template <int WM, int WN, int TM, int TN>
+struct GemmCfg {
+    static constexpr int BM = 32 * TM * WM;     // rows per workgroup
+    static constexpr int BN = 32 * TN * WN;     // tokens per workgroup
+    static constexpr int THREADS = 64 * WM * WN;
+    // global loads per thread per block
+    static constexpr int A_DW = BM * 9;                    // 9 dwords cover a 34-byte block
+    static constexpr int A_PER = (A_DW + THREADS - 1) / THREADS;
+    static constexpr int X_DW = 4 * BN * 9;                // 4 chunks x BN tokens x 36 bytes
+    static constexpr int X_PER = (X_DW + THREADS - 1) / THREADS;
+};
+
+template <int WM, int WN, int TM, int TN>
+__global__ void __launch_bounds__(64 * WM * WN)
 gemm_mfma_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
                  float * __restrict__ Y, int n_out, int n_tok, int nb) {
-    constexpr int BM = 32 * WM, BN = 32 * WN;
-    __shared__ uint32_t sA[BM][9];                       // 8 code dwords per row (+1 pad)
-    __shared__ __attribute__((aligned(16))) float sDw[BM];
+    using C = GemmCfg<WM, WN, TM, TN>;
+    constexpr int BM = C::BM, BN = C::BN;
+    __shared__ uint32_t sA[BM][10];                       // raw 9-dword window of each row's block (+1 pad)
     __shared__ __attribute__((aligned(16))) uint32_t sX[4][BN][8];
     __shared__ float sDa[4][BN];
 
@@ -49,17 +67,181 @@ gemm_mfma_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
     const int wm = wave % WM, wn = wave / WM;
     const int row0 = blockIdx.x * BM, tok0 = blockIdx.y * BN;
     const int h = lane >> 5, l32 = lane & 31;
-    const size_t wstride = (size_t)PQ2_BYTES * nb;
+    const size_t wstride = (size_t)PQ2_BYTES * nb;          // bytes per weight row (even nb: 4-aligned)
 
+    // ---- global -> register prefetch of one block ---------------------------
+    // A: row rr, dword k (0..8) of the 9-dword window that starts at the
+    // block's dword-aligned floor.  For even nb a block starts 4-aligned when
+    // b is even and 2 bytes past a dword when b is odd.
+    uint32_t ra[C::A_PER];
+    uint32_t rx[C::X_PER];
+    auto prefetch = [&](int b) {
+#pragma unroll
+        for (int j = 0; j < C::A_PER; ++j) {
+            const int i = tid + j * C::THREADS;
+            uint32_t v = 0x55555555u;                     // codes all 1 -> (code - 1) = 0
+            if (i < C::A_DW) {
+                const int rr = i / 9, k = i - 9 * rr;
+                const int row = row0 + rr;
+                if (row < n_out) {
+                    const size_t boff = (size_t)row * wstride + (size_t)PQ2_BYTES * b;
+                    // window [floor(block start), +36): for an even block it ends 2 bytes
+                    // into the next block, for an odd one exactly at the block end, so
+                    // it never leaves the row (the last block of a row is odd)
+                    const size_t a0 = (boff & ~(size_t)3) + 4 * (size_t)k;
+                    v = *reinterpret_cast<const uint32_t *>(W + a0);
+                } else if (k == 0) {
+                    v = 0;
+                }
+            }
+            ra[j] = v;
+        }
+#pragma unroll
+        for (int j = 0; j < C::X_PER; ++j) {
+            const int i = tid + j * C::THREADS;
+            uint32_t v = 0;
+            if (i < C::X_DW) {
+                const int k = i % 9, rest = i / 9;
+                const int t = rest % BN, p = rest / BN;
+                const int tok = tok0 + t;
+                if (tok < n_tok)
+                    v = reinterpret_cast<const uint32_t *>(X + ((size_t)(4 * b + p) * n_tok + tok) * Q81_BYTES)[k];
+            }
+            rx[j] = v;
+        }
+    };
+    // ---- registers -> LDS ---------------------------------------------------
+    auto commit = [&]() {
+#pragma unroll
+        for (int j = 0; j < C::A_PER; ++j) {
+            const int i = tid + j * C::THREADS;
+            if (i < C::A_DW) {
+                const int rr = i / 9, k = i - 9 * rr;
+                sA[rr][k] = ra[j];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < C::X_PER; ++j) {
+            const int i = tid + j * C::THREADS;
+            if (i < C::X_DW) {
+                const int k = i % 9, rest = i / 9;
+                const int t = rest % BN, p = rest / BN;
+                if (k == 0) sDa[p][t] = f16_bits_to_f32(rx[j] & 0xffffu);
+                else sX[p][t][k - 1] = rx[j];
+            }
+        }
+    };
+
+    float acc[TM][TN][16];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int c = 0; c < TN; ++c)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[a][c][i] = 0.0f;
+
+    prefetch(0);
+    for (int b = 0; b < nb; ++b) {
+        __syncthreads();                       // previous block's LDS reads are done
+        commit();
+        __syncthreads();
+        if (b + 1 < nb) prefetch(b + 1);
+        // The raw window of a row starts at the block's dword floor; the block
+        // begins sh bytes into dword 0 (0 for even b, 2 for odd b: rows are
+        // 4-byte aligned because nb is even).  fp16 d = block bytes [0, 2),
+        // code dword c = block bytes [2 + 4c, 6 + 4c).
+        const int sh = (int)(((size_t)PQ2_BYTES * b) & 3);
+
+        float inner[TM][TN][16];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            v4i A[TM];
+#pragma unroll
+            for (int a = 0; a < TM; ++a) {
+                const int rr = (wm * TM + a) * 32 + l32;
+                // code dword (2p + h) = block bytes [2 + 8p + 4h, 6 + 8p + 4h)
+                const int byte = sh + 2 + 8 * p + 4 * h;
+                const uint32_t lo = sA[rr][byte >> 2], hi = sA[rr][(byte >> 2) + 1];
+                const uint32_t w = __builtin_amdgcn_alignbyte(hi, lo, byte & 3);
+                A[a].x = codes_minus_one(w, 0); A[a].y = codes_minus_one(w, 1);
+                A[a].z = codes_minus_one(w, 2); A[a].w = codes_minus_one(w, 3);
+            }
+#pragma unroll
+            for (int c = 0; c < TN; ++c) {
+                const int tt = (wn * TN + c) * 32 + l32;
+                const v4i Bv = *reinterpret_cast<const v4i *>(&sX[p][tt][4 * h]);
+                const float da = sDa[p][tt];
+#pragma unroll
+                for (int a = 0; a < TM; ++a) {
+                    v16i S = {};
+                    S = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[a], Bv, S, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        inner[a][c][i] = (p == 0) ? da * (float)S[i] : fmaf(da, (float)S[i], inner[a][c][i]);
+                }
+            }
+        }
+        // per-row block scale: rows 8(i/4) + 4h + (i%4) of each 32-row tile
+#pragma unroll
+        for (int a = 0; a < TM; ++a) {
+            const int rbase = (wm * TM + a) * 32;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int rr = rbase + 8 * q + 4 * h;
+                float dw[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t d0 = sA[rr + e][0];
+                    dw[e] = f16_bits_to_f32(sh ? (d0 >> 16) : (d0 & 0xffffu));
+                }
+#pragma unroll
+                for (int c = 0; c < TN; ++c)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        acc[a][c][4 * q + e] = fmaf(dw[e], inner[a][c][4 * q + e], acc[a][c][4 * q + e]);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int c = 0; c < TN; ++c) {
+        const int tok = tok0 + (wn * TN + c) * 32 + l32;
+        if (tok >= n_tok) continue;
+#pragma unroll
+        for (int a = 0; a < TM; ++a) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int row = row0 + (wm * TM + a) * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+                if (row < n_out) Y[(size_t)row * n_tok + tok] = acc[a][c][i];
+            }
+        }
+    }
+}
+
+// Odd nb (n_in = 128 * odd): blocks are 2-byte aligned with a row-dependent
+// phase, so this variant stages codes with 16-bit loads.
+__global__ void __launch_bounds__(256)
+gemm_mfma_kernel_u16(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
+                     float * __restrict__ Y, int n_out, int n_tok, int nb) {
+    constexpr int BM = 64, BN = 64;
+    __shared__ uint32_t sA[BM][9];
+    __shared__ __attribute__((aligned(16))) float sDw[BM];
+    __shared__ __attribute__((aligned(16))) uint32_t sX[4][BN][8];
+    __shared__ float sDa[4][BN];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave % 2, wn = wave / 2;
+    const int row0 = blockIdx.x * BM, tok0 = blockIdx.y * BN;
+    const int h = lane >> 5, l32 = lane & 31;
+    const size_t wstride = (size_t)PQ2_BYTES * nb;
     float acc[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-
     for (int b = 0; b < nb; ++b) {
         for (int i = tid; i < BM * 17; i += 256) {
             const int rr = i / 17, k = i - 17 * rr;
             const int row = row0 + rr;
-            uint32_t v = 0x5555u;                         // all codes 1 -> value 0
+            uint32_t v = 0x5555u;
             if (row < n_out)
                 v = reinterpret_cast<const uint16_t *>(W + (size_t)row * wstride + (size_t)PQ2_BYTES * b)[k];
             else if (k == 0)
@@ -78,7 +260,6 @@ gemm_mfma_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
             else sX[p][t][k - 1] = v;
         }
         __syncthreads();
-
         float inner[16];
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
@@ -86,9 +267,9 @@ gemm_mfma_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
             v4i A;
             A.x = codes_minus_one(w, 0); A.y = codes_minus_one(w, 1);
             A.z = codes_minus_one(w, 2); A.w = codes_minus_one(w, 3);
-            const v4i B = *reinterpret_cast<const v4i *>(&sX[p][wn * 32 + l32][4 * h]);
+            const v4i Bv = *reinterpret_cast<const v4i *>(&sX[p][wn * 32 + l32][4 * h]);
             v16i S = {};
-            S = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, S, 0, 0, 0);
+            S = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bv, S, 0, 0, 0);
             const float da = sDa[p][wn * 32 + l32];
 #pragma unroll
             for (int i = 0; i < 16; ++i) inner[i] = (p == 0) ? da * (float)S[i] : fmaf(da, (float)S[i], inner[i]);
@@ -103,7 +284,6 @@ gemm_mfma_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
         }
         __syncthreads();
     }
-
     const int tok = tok0 + wn * 32 + l32;
     if (tok < n_tok) {
 #pragma unroll
@@ -112,6 +292,148 @@ gemm_mfma_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
             if (row < n_out) Y[(size_t)row * n_tok + tok] = acc[i];
         }
     }
+}
+
+// ---------------------------------------------------------------------------
+// Small batch (2 <= n_tok <= 16), bandwidth-bound: a workgroup owns 16 rows
+// and its 4 waves split K into quarters on even-block boundaries (every model
+// width has nb % 8 == 0).  Each wave DMAs its 16 row segments (34 * nb/4
+// bytes each, dword aligned) into LDS with global_load_lds_dword, then per
+// Q8_1 chunk issues one v_mfma_i32_16x16x32_i8: A = 16 rows x 32 weights as
+// int8 (code - 1), B = 32 activations x 16 token columns read straight from
+// the chunk-major X (columns past n_tok carry a duplicate token and are not
+// stored).  Lane (r = l%16, g = l/16) supplies the 8 bytes of K-group g:
+// activation words 2(g%2), 2(g%2)+1 of half g/2 -- the code words
+// (w >> 2k) & 0x03030303 of the same half line up byte for byte.  The four
+// K-quarter partials are summed through LDS.
+typedef int v2i __attribute__((ext_vector_type(2), aligned(4)));
+typedef int v4ia __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+__global__ void __launch_bounds__(256)
+gemm_skinny_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
+                   float * __restrict__ Y, int n_out, int n_tok, int nb) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nbq = nb / 4;                       // blocks per K quarter (even)
+    const int seg = PQ2_BYTES * nbq;              // bytes per row segment (multiple of 4)
+    const int segdw = seg / 4;
+    uint8_t * wl = smem + (size_t)wave * 16 * seg;
+    float * red = reinterpret_cast<float *>(smem + (size_t)4 * 16 * seg);   // [4][16][16]
+    const int row0 = blockIdx.x * 16;
+    const size_t wstride = (size_t)PQ2_BYTES * nb;
+
+    // 1. DMA the wave's 16 row segments: LDS dword idx = r * segdw + d
+    const int ndw = 16 * segdw;
+    for (int i = 0; i < ndw; i += 64) {
+        const int idx = i + lane;
+        if (idx < ndw) {                          // lanes past the segment write nothing
+            const int r = idx / segdw, d = idx - r * segdw;
+            const int row = min(row0 + r, n_out - 1);
+            const uint8_t * src = W + (size_t)row * wstride + (size_t)seg * wave + 4 * (size_t)d;
+            __builtin_amdgcn_global_load_lds(src, (lds_void *)(wl + 4 * i), 4, 0, 0);
+        }
+    }
+
+    const int r = lane & 15, g = lane >> 4;
+    const int t = min(lane & 15, n_tok - 1);      // B column (token)
+    const int h = g >> 1, kk = 2 * (g & 1);       // half and first activation word of the K-group
+    const int c0 = 4 * nbq * wave;                // first global chunk of this quarter
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+
+    // X for two blocks (8 chunks) per register set, loaded two blocks ahead
+    uint32_t nd[8], cd[8];
+    v2i nx[8], cx[8];
+    // per-lane byte offset inside a chunk's n_tok blocks; the chunk base is uniform
+    const uint32_t xlane = (uint32_t)t * Q81_BYTES;
+    const size_t cstride = (size_t)n_tok * Q81_BYTES;
+    auto load_x = [&](int b) {
+        const uint8_t * xc = X + (size_t)(c0 + 4 * min(b, nbq - 2)) * cstride;   // past the end: re-read the last pair
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const uint8_t * xp = xc + (size_t)q * cstride + xlane;
+            nd[q] = *reinterpret_cast<const uint32_t *>(xp);
+            nx[q] = *reinterpret_cast<const v2i *>(xp + 4 + 8 * g);
+        }
+    };
+    load_x(0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);           // vmcnt(0): the segments (and X pair 0) have landed
+    __builtin_amdgcn_wave_barrier();
+
+    for (int b = 0; b < nbq; b += 2) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) { cd[q] = nd[q]; cx[q] = nx[q]; }
+        load_x(b + 2);
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb) {
+            v4ia S[4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                // code word h of chunk p of block b + bb, realigned from two LDS dwords
+                const int off = r * seg + PQ2_BYTES * (b + bb) + 2 + 8 * p + 4 * h;
+                const uint32_t lo = *reinterpret_cast<const uint32_t *>(wl + (off & ~3));
+                const uint32_t hi = *reinterpret_cast<const uint32_t *>(wl + (off & ~3) + 4);
+                const uint32_t w = __builtin_amdgcn_alignbyte(hi, lo, off & 3);
+                v2i Av;
+                Av.x = codes_minus_one(w, kk);
+                Av.y = codes_minus_one(w, kk + 1);
+                S[p] = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, Av),
+                                                           __builtin_bit_cast(long, cx[4 * bb + p]),
+                                                           (v4ia){0, 0, 0, 0}, 0, 0, 0);
+            }
+            float inner[4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const float da = f16_bits_to_f32(cd[4 * bb + p] & 0xffffu);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) inner[i] = (p == 0) ? da * (float)S[p][i] : fmaf(da, (float)S[p][i], inner[i]);
+            }
+            // output rows 4g + i of the 16: their block scale
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t dwb = *reinterpret_cast<const uint16_t *>(wl + (4 * g + i) * seg + PQ2_BYTES * (b + bb));
+                acc[i] = fmaf(f16_bits_to_f32(dwb), inner[i], acc[i]);
+            }
+        }
+    }
+    // 2. sum the four K quarters
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(wave * 16 + 4 * g + i) * 16 + (lane & 15)] = acc[i];
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int rr = 4 * g + i, col = lane & 15;
+            const float v = red[(0 * 16 + rr) * 16 + col] + red[(1 * 16 + rr) * 16 + col] +
+                            red[(2 * 16 + rr) * 16 + col] + red[(3 * 16 + rr) * 16 + col];
+            const int row = row0 + rr;
+            if (row < n_out && col < n_tok) Y[(size_t)row * n_tok + col] = v;
+        }
+    }
+}
+
+template <int WM, int WN, int TM, int TN>
+void launch_gemm(const uint8_t * W, const uint8_t * X, float * Y, int n_out, int n_tok, int nb,
+                 hipStream_t st) {
+    using C = GemmCfg<WM, WN, TM, TN>;
+    dim3 grid((unsigned)cdiv(n_out, C::BM), (unsigned)cdiv(n_tok, C::BN));
+    hipLaunchKernelGGL((gemm_mfma_kernel<WM, WN, TM, TN>), grid, dim3(C::THREADS), 0, st, W, X, Y,
+                       n_out, n_tok, nb);
+}
+
+int skinny_lds_limit() {
+    static int v = -1;
+    if (v < 0) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        int x = 0;
+        if (hipDeviceGetAttribute(&x, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || x <= 0)
+            x = 64 * 1024;
+        v = x;
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_skinny_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, x);
+    }
+    return v;
 }
 
 }  // namespace
@@ -123,17 +445,25 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
     if (n_in <= 0 || n_in % QK_PQ2 != 0) return 1;
     if (n_out <= 0 || n_tok <= 0) return 0;
     if (((uintptr_t)Xq & 3u) != 0 || ((uintptr_t)W & 1u) != 0) return 1;
-    if (n_out > 0x7fffffff || n_tok > 0x7fffffff) return 1;
+    if (n_out > 0x7fffffff || n_tok > 0x7fffffff || n_in / QK_PQ2 > (1 << 24)) return 1;
     const int nb = (int)(n_in / QK_PQ2);
     hipStream_t st = (hipStream_t)stream;
-    if (n_tok <= 32) {
-        dim3 grid((unsigned)cdiv(n_out, 128), (unsigned)cdiv(n_tok, 32));
-        hipLaunchKernelGGL((gemm_mfma_kernel<4, 1>), grid, dim3(256), 0, st, (const uint8_t *)W,
-                           (const uint8_t *)Xq, Y, (int)n_out, (int)n_tok, nb);
-    } else {
+    const uint8_t * w = (const uint8_t *)W;
+    const uint8_t * x = (const uint8_t *)Xq;
+    if (n_tok == 1) return bonsai_p40_gemv(W, Xq, Y, n_out, n_in, stream);   // chunk-major == token-major
+    const size_t skinny_lds = (size_t)4 * 16 * PQ2_BYTES * (nb / 4) + 4096;
+    if (n_tok <= 16 && nb % 8 == 0 && ((uintptr_t)W & 3u) == 0 && skinny_lds <= (size_t)skinny_lds_limit()) {
+        hipLaunchKernelGGL(gemm_skinny_kernel, dim3((unsigned)cdiv(n_out, 16)), dim3(256), skinny_lds, st, w, x, Y,
+                           (int)n_out, (int)n_tok, nb);
+        return (int)hipGetLastError();
+    }
+    if ((nb & 1) || ((uintptr_t)W & 3u) != 0) {
         dim3 grid((unsigned)cdiv(n_out, 64), (unsigned)cdiv(n_tok, 64));
-        hipLaunchKernelGGL((gemm_mfma_kernel<2, 2>), grid, dim3(256), 0, st, (const uint8_t *)W,
-                           (const uint8_t *)Xq, Y, (int)n_out, (int)n_tok, nb);
+        hipLaunchKernelGGL(gemm_mfma_kernel_u16, grid, dim3(256), 0, st, w, x, Y, (int)n_out, (int)n_tok, nb);
+    } else if (n_tok <= 32) {
+        launch_gemm<4, 1, 1, 1>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
+    } else {
+        launch_gemm<4, 2, 1, 2>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
     }
     return (int)hipGetLastError();
 }

@@ -255,8 +255,9 @@ def test_gemm_fixture(golden, tag):
 
 
 @pytest.mark.parametrize("n_out,n_in,n_tok", [(96, 1024, 1), (130, 2048, 2), (64, 5120, 4),
-                                              (200, 1024, 8), (70, 1024, 37), (128, 5120, 128),
-                                              (33, 384, 65)])
+                                              (200, 1024, 8), (70, 2048, 13), (17, 17408, 5),
+                                              (300, 6144, 16), (70, 1024, 37), (128, 5120, 128),
+                                              (33, 384, 65), (40, 384, 3), (50, 1152, 6)])
 def test_gemm_matches_oracle(n_out, n_in, n_tok):
     case(f"gemm {n_out}x{n_in}x{n_tok}")
     W = O.gen_weights(1100 + n_out, n_out, n_in, 0.01)
