@@ -199,6 +199,7 @@ struct NbSpec {
     static constexpr int LDSB = (S * SLOT_BYTES + 16 > 1024 * NPL) ? S * SLOT_BYTES + 16 : 1024 * NPL;
     static constexpr int SPLIT = (G == 2) ? NCH / 64 : -1;
     static constexpr bool PARTIAL = (G * NCH) % 64 != 0;   // last slot has idle lanes 32..63
+    static_assert(UB % 16 == 0, "a unit is a whole number of 16-byte pieces");
 };
 
 typedef int v4i_a4 __attribute__((ext_vector_type(4), aligned(4)));
@@ -212,6 +213,9 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
+
+// cache-policy operand of global_load_lds on gfx950: bit 1 = nt (non-temporal)
+constexpr int CPOL_NT = 2;
 
 // Reduce acc0 over lanes 0..63 and acc1 over lanes 0..63 at once:
 // v_permlane32_swap folds the upper half of acc0 onto its lower half and the
@@ -228,8 +232,8 @@ __device__ __forceinline__ float wave_sum2_to_lanes31_63(float acc0, float acc1)
     return v;
 }
 
-// Workgroup of WAVES waves.  Each wave owns `units_per_wave` consecutive
-// units and a private ring of D unit buffers in LDS; the workgroup shares one
+// Workgroup of WAVES waves.  Each wave owns up to `units_per_wave` units
+// (grid-strided) and a private ring of D unit buffers in LDS; the workgroup shares one
 // LDS copy of the Q8_1 activation.  Every global read is an LDS DMA
 // (global_load_lds_dwordx4), so the only waits are the explicit vmcnt waits
 // below, and each unit is consumed as soon as its own bytes have landed.
@@ -245,13 +249,21 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
     __shared__ __attribute__((aligned(16))) uint8_t act_lds[NA * 1024];
     __shared__ __attribute__((aligned(16))) uint8_t ring_all[WAVES][D][P::LDSB];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     __builtin_assume(lane >= 0 && lane < 64);
     uint8_t (*ring)[P::LDSB] = ring_all[wave];
     const int n_units = (n_out + P::G - 1) / P::G;
-    const int u0 = (blockIdx.x * WAVES + wave) * units_per_wave;
-    const int nu = min(units_per_wave, n_units - u0);       // <= 0 for idle trailing waves
-    const size_t total_bytes = (size_t)n_out * PQ2_BYTES * NB;
+    const int n_full = n_out / P::G;                        // units with all G rows present
+    // units are dealt to waves grid-strided: wave gw owns units gw, gw + NW,
+    // gw + 2 NW, ...  Every issue round then reads one contiguous stretch of
+    // W across the whole grid; a contiguous per-wave span of 3 units
+    // (8160 B at 17408x5120) measured 15 % slower (HBM channel camping).
+    // slot-major wave numbering: the waves that carry one unit more than the
+    // others are spread over all workgroups (hence all CUs) rather than packed
+    // into the first ones
+    const int gw = wave * gridDim.x + blockIdx.x;
+    const int NW = gridDim.x * WAVES;
+    const int nu = gw < n_units ? min(units_per_wave, (n_units - 1 - gw) / NW + 1) : 0;
 
     // 1. activation share of this wave (instructions k = wave, wave + WAVES, ...)
     for (int k = wave; k < NA; k += WAVES) {
@@ -260,24 +272,39 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. the first D units (unit i exactly NPL instructions; lanes past the
-    //    unit or past W re-read the last in-bounds piece, landing in LDS past
-    //    the unit bytes or in a row that is never stored)
-    const size_t last_piece = total_bytes / 16 - 1;
+    // 2. the first D units.  Unit i is exactly NPL instructions; lanes past
+    //    the unit re-read its last piece (landing in LDS past the unit bytes).
+    //    A full unit's pieces are a uniform base plus a per-lane 32-bit offset;
+    //    only a trailing unit with fewer than G rows clamps to the end of W.
+    uint32_t poff[P::NPL];
+#pragma unroll
+    for (int k = 0; k < P::NPL; ++k) poff[k] = 16u * (uint32_t)min(lane + 64 * k, P::NPIECE - 1);
+    const size_t last_piece = (size_t)n_out * PQ2_BYTES * NB / 16 - 1;
     auto issue = [&](int uu, int slot) {
-        const size_t base = (size_t)uu * (P::UB / 16);
+        const uint8_t * base = W + (size_t)uu * P::UB;
+        const bool full = uu < n_full;
 #pragma unroll
         for (int k = 0; k < P::NPL; ++k) {
-            size_t p = base + (size_t)min(lane + 64 * k, P::NPIECE - 1);
-            p = p < last_piece ? p : last_piece;
-            __builtin_amdgcn_global_load_lds(W + 16 * p, (lds_void *)(&ring[slot][1024 * k]), 16, 0, 0);
+            const uint8_t * src = base + poff[k];
+            if (!full) {
+                size_t p = (size_t)uu * (P::UB / 16) + poff[k] / 16;
+                src = W + 16 * (p < last_piece ? p : last_piece);
+            }
+            // nt: weights stream through L2 without displacing the activation
+            __builtin_amdgcn_global_load_lds(src, (lds_void *)(&ring[slot][1024 * k]), 16, 0, CPOL_NT);
         }
     };
-    if (nu > 0) {
+    // issue rounds: every wave's activation share, then every wave's first
+    // unit, then every second unit, ...  A CU serves its requests roughly in
+    // issue order, so the barrier between rounds keeps each wave's first
+    // bytes (and the shared activation) ahead of the other waves' later units
+    // instead of queued behind them.
 #pragma unroll
-        for (int i = 0; i < D; ++i) issue(u0 + min(i, nu - 1), i);
+    for (int i = 0; i < D; ++i) {
+        __builtin_amdgcn_s_barrier();
+        if (nu > 0) issue(gw + min(i, nu - 1) * NW, i);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
 
     // 3. own activation share landed (all unit DMAs are younger), then the
     //    workgroup barrier makes every share visible
@@ -286,9 +313,11 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
     __builtin_amdgcn_s_barrier();
     if (nu <= 0) return;
 
-    int act[P::S][8];
-    float da16[P::S];
-    int bias16[P::S];
+    // the lane's chunk of slot j is the same in every unit: its activation
+    // nibble planes, scale and -s bias stay in registers
+    uint32_t ah[P::S][4], al[P::S][4];
+    float da[P::S];
+    int bias[P::S];
 #pragma unroll
     for (int j = 0; j < P::S; ++j) {
         const int v = 64 * j + lane;
@@ -297,17 +326,23 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
         c = valid ? c : 0;
         const uint32_t * a = reinterpret_cast<const uint32_t *>(&act_lds[Q81_BYTES * c]);
         const uint32_t ds = a[0];
+        uint32_t aw[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) act[j][k] = valid ? (int)a[1 + k] : 0;
-        da16[j] = valid ? f16_bits_to_f32(ds & 0xffffu) * (1.0f / 16.0f) : 0.0f;
-        bias16[j] = valid ? -16 * (int)(int16_t)(ds >> 16) : 0;
+        for (int k = 0; k < 8; ++k) aw[k] = valid ? a[1 + k] : 0u;
+        nib_planes(aw, ah[j], al[j]);
+        da[j] = valid ? f16_bits_to_f32(ds & 0xffffu) : 0.0f;
+        bias[j] = valid ? -(int)(int16_t)(ds >> 16) : 0;
     }
 
+    // code bytes of the lane's chunk: 8 bytes at a 2-byte aligned LDS offset,
+    // read as 3 aligned dwords and realigned with v_alignbyte (a per-lane
+    // constant shift; unaligned 8-byte DS reads measured slower); block scale
+    // at the block start
     const int cw = PQ2_BYTES * (lane >> 2) + 2 + 8 * (lane & 3);
     const int sh = cw & 3;
     const int cw_al = cw - sh;
     const int dwo = PQ2_BYTES * (lane >> 2);
-    float ykeep = 0.0f;                       // lane j keeps the output of row u0*G + j
+    float ykeep = 0.0f;                       // lane G*i + r keeps row r of unit i
 
     int i = 0;
     do {
@@ -318,27 +353,24 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
         else wait_vmcnt<0>();
         __builtin_amdgcn_wave_barrier();
         const uint8_t * ub = ring[slot];
-        const int u = u0 + i;
+        const int u = gw + i * NW;
 
         float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
         for (int j = 0; j < P::S; ++j) {
-            const uint8_t * cp = ub + cw_al + SLOT_BYTES * j;
-            const uint32_t d0 = *reinterpret_cast<const uint32_t *>(cp);
-            const uint32_t d1 = *reinterpret_cast<const uint32_t *>(cp + 4);
-            const uint32_t d2 = *reinterpret_cast<const uint32_t *>(cp + 8);
-            const uint32_t w0 = __builtin_amdgcn_alignbyte(d1, d0, sh);
-            const uint32_t w1 = __builtin_amdgcn_alignbyte(d2, d1, sh);
+            const uint32_t * cpa = reinterpret_cast<const uint32_t *>(ub + cw_al + SLOT_BYTES * j);
+            const uint32_t w0 = __builtin_amdgcn_alignbyte(cpa[1], cpa[0], sh);
+            const uint32_t w1 = __builtin_amdgcn_alignbyte(cpa[2], cpa[1], sh);
             const uint32_t dwb = *reinterpret_cast<const uint16_t *>(ub + dwo + SLOT_BYTES * j);
-            const int s16 = chunk_dot_x16(w0, w1, act[j], bias16[j]);
+            const int s = chunk_dot_nib(w0, w1, ah[j], al[j], bias[j]);
             const bool second = (P::G == 2) && (j > P::SPLIT || (j == P::SPLIT && lane >= 32));
             if (DUMP) {
                 const int v = 64 * j + lane;
                 const int row = u * P::G + (second ? 1 : 0);
                 if (v < P::G * P::NCH && row < n_out)
-                    dump[(size_t)row * P::NCH + (second ? v - P::NCH : v)] = s16 >> 4;
+                    dump[(size_t)row * P::NCH + (second ? v - P::NCH : v)] = s;
             } else {
-                const float t = da16[j] * (float)s16;
+                const float t = da[j] * (float)s;
                 float dw = f16_bits_to_f32(dwb);
                 if (P::PARTIAL && j == P::S - 1) dw = lane < 32 ? dw : 0.0f;   // idle lanes: LDS past the unit
                 if (P::G == 1 || j < P::SPLIT) acc0 = fmaf(dw, t, acc0);
@@ -362,11 +394,11 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
         if (i + D < nu) {
             __builtin_amdgcn_s_waitcnt(0xC07F);    // lgkmcnt(0)
             __builtin_amdgcn_wave_barrier();
-            issue(u0 + i + D, slot);
+            issue(gw + (i + D) * NW, slot);
         }
     } while (++i < nu);
     if (!DUMP) {
-        const int row = u0 * P::G + lane;
+        const int row = (gw + (lane / P::G) * NW) * P::G + lane % P::G;
         if (lane < nu * P::G && row < n_out) y[row] = ykeep;
     }
 }
@@ -475,23 +507,33 @@ int cu_count() {
     return v;
 }
 
+// Workgroups per CU for the decode GEMV, from sweeps on MI355X (HIP-graph
+// replay, weights streamed from HBM): rows of <= 48 blocks want 3 workgroups
+// per CU on the 24 MB matrices and 2 on the 7-8 MB ones; the widest rows
+// (60 KB of LDS per workgroup) run best at one per CU.
+int default_wg_per_cu(int nb, int64_t w_bytes) {
+    if (nb >= 96) return 1;
+    return w_bytes >= (16 << 20) ? 3 : 2;
+}
+
 template <int NB, int D, int WAVES, bool DUMP>
 int launch_nb_t(const uint8_t * W, const uint8_t * xq, float * y, int32_t * dump, int n_out,
                 hipStream_t st) {
     using P = NbSpec<NB>;
-    constexpr size_t lds = (size_t)((Q81_BYTES * P::NCH + 1023) / 1024) * 1024 + (size_t)WAVES * D * P::LDSB;
     const int n_units = (n_out + P::G - 1) / P::G;
-    int upw = env_int("BONSAI_GEMV_UNITS_PER_WAVE", 0);
-    if (upw <= 0) {
-        // enough units per wave that every wave fits on the GPU at once
-        int wg_per_cu = (int)((160 * 1024) / lds);
-        wg_per_cu = wg_per_cu < 1 ? 1 : (wg_per_cu > 20 / WAVES ? 20 / WAVES : wg_per_cu);
-        const int resident = cu_count() * wg_per_cu * WAVES;
-        upw = (n_units + resident - 1) / resident;
+    // a whole number of workgroups per CU (the dispatcher then places exactly
+    // that many on every CU), fewer for small matrices
+    int per_cu = env_int("BONSAI_GEMV_WG_PER_CU", 0);
+    if (per_cu <= 0) per_cu = default_wg_per_cu(NB, (int64_t)n_out * PQ2_BYTES * NB);
+    int blocks = per_cu * cu_count();
+    const int max_blocks = (n_units + WAVES - 1) / WAVES;
+    if (blocks > max_blocks) blocks = max_blocks;
+    const int NW = blocks * WAVES;
+    int upw = (n_units + NW - 1) / NW;
+    if (upw > 64 / P::G) {                      // one output per lane of a wave
+        upw = 64 / P::G;
+        blocks = (n_units + upw * WAVES - 1) / (upw * WAVES);
     }
-    upw = upw < 1 ? 1 : (upw > 64 / P::G ? 64 / P::G : upw);
-    const int waves = (n_units + upw - 1) / upw;
-    const int blocks = (waves + WAVES - 1) / WAVES;
     hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, DUMP>), dim3(blocks), dim3(64 * WAVES), 0, st, W, xq,
                        y, dump, n_out, upw);
     return (int)hipGetLastError();
@@ -500,9 +542,9 @@ int launch_nb_t(const uint8_t * W, const uint8_t * xq, float * y, int32_t * dump
 template <int NB, bool DUMP>
 int launch_nb(const uint8_t * W, const uint8_t * xq, float * y, int32_t * dump, int n_out,
               hipStream_t st) {
-    // ring depth 2 for the widest rows keeps two 4-wave workgroups per CU
-    if (NB >= 96) return launch_nb_t<NB, 2, 4, DUMP>(W, xq, y, dump, n_out, st);
-    return launch_nb_t<NB, 3, 4, DUMP>(W, xq, y, dump, n_out, st);
+    // 4-wave workgroups with two unit buffers per wave measured best at every
+    // model width (deeper rings queue more bytes ahead of the activation)
+    return launch_nb_t<NB, 2, 4, DUMP>(W, xq, y, dump, n_out, st);
 }
 
 template <bool DUMP>

@@ -122,6 +122,46 @@ __device__ __forceinline__ int chunk_dot_x16(uint32_t w0, uint32_t w1, const int
     return (s1 << 4) + s16;
 }
 
+// Nibble-plane form of the same chunk dot, for activations that are reused
+// across many weight rows.  An int8 activation splits as a = 16*h + l with
+// h = a >> 4 (signed, -8..7) and l = a & 15 (unsigned, 0..15); both are the
+// two nibbles of the byte as stored.  A code word w gives two nibble words
+// with one shift and two masks: w & 0x33333333 holds bit pairs 0 and 2 of
+// every byte (nibbles 2j and 2j+1), (w >> 2) & 0x33333333 bit pairs 1 and 3.
+// The matching activation planes interleave the nibbles of permuted words
+// a_k and a_{k+2} the same way, so
+//   sum code*a = 16 * sdot8(codes, h-plane) + udot8(codes, l-plane)
+// with codes 0..3 valid both as signed and unsigned 4-bit values.
+// nib_planes() builds the 4 h-words and 4 l-words of one chunk from its 8
+// permuted activation words; chunk_dot_nib() returns sumi exactly.
+__device__ __forceinline__ void nib_planes(const uint32_t (&a)[8], uint32_t (&h)[4], uint32_t (&l)[4]) {
+    constexpr uint32_t LO = 0x0F0F0F0Fu;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t x = a[4 * q + k], z = a[4 * q + k + 2];
+            h[2 * q + k] = ((x >> 4) & LO) | (z & ~LO);
+            l[2 * q + k] = (x & LO) | ((z << 4) & ~LO);
+        }
+    }
+}
+
+__device__ __forceinline__ int chunk_dot_nib(uint32_t w0, uint32_t w1, const uint32_t (&h)[4],
+                                             const uint32_t (&l)[4], int bias) {
+    constexpr uint32_t M = 0x33333333u;
+    const uint32_t n0 = w0 & M, n1 = (w0 >> 2) & M, n2 = w1 & M, n3 = (w1 >> 2) & M;
+    int sh = __builtin_amdgcn_sdot8((int)n0, (int)h[0], 0, false);
+    sh = __builtin_amdgcn_sdot8((int)n1, (int)h[1], sh, false);
+    sh = __builtin_amdgcn_sdot8((int)n2, (int)h[2], sh, false);
+    sh = __builtin_amdgcn_sdot8((int)n3, (int)h[3], sh, false);
+    uint32_t sl = __builtin_amdgcn_udot8(n0, l[0], (uint32_t)bias, false);
+    sl = __builtin_amdgcn_udot8(n1, l[1], sl, false);
+    sl = __builtin_amdgcn_udot8(n2, l[2], sl, false);
+    sl = __builtin_amdgcn_udot8(n3, l[3], sl, false);
+    return (int)(((uint32_t)sh << 4) + sl);   // modulo 2^32: exact for |sumi| < 2^31
+}
+
 __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace pq2
