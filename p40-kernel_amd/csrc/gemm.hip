@@ -27,6 +27,8 @@
 #include "pq2_device.h"
 #include "../../include/bonsai_p40.h"
 
+#include <stdlib.h>
+
 using namespace pq2;
 
 namespace {
@@ -421,6 +423,11 @@ void launch_gemm(const uint8_t * W, const uint8_t * X, float * Y, int n_out, int
                        n_out, n_tok, nb);
 }
 
+int env_int_gemm(const char * name, int dflt) {
+    const char * v = getenv(name);
+    return (v && *v) ? atoi(v) : dflt;
+}
+
 int skinny_lds_limit() {
     static int v = -1;
     if (v < 0) {
@@ -434,6 +441,253 @@ int skinny_lds_limit() {
                                   hipFuncAttributeMaxDynamicSharedMemorySize, x);
     }
     return v;
+}
+
+// ---------------------------------------------------------------------------
+// f16-MFMA prefill GEMM.  v_mfma_f32_16x16x32_f16 with A = (code - 1) and B = q
+// as f16: both are small integers, exact in f16, and the MFMA's fp32
+// accumulation of 32 products stays exact (|S| <= 8128 < 2^24), so each
+// MFMA returns the chunk dot S already as an fp32 value.  The per-chunk
+// activation scale then costs one FMA per output element (the int8 MFMA
+// needs a convert and an FMA), and the per-block weight scale one FMA per
+// element per 4 chunks.
+//
+// Workgroup: 512 threads (8 waves as 2 x 4), tile 128 rows x 128 tokens; a
+// wave owns 64 rows x 32 tokens = 4 x 2 MFMA tiles of 16 x 16.  Per PQ2_0
+// block (K = 128) the workgroup converts the tile's codes and Q8_1 bytes to
+// f16 once, into LDS laid out [chunk][row or token][32 positions] with the
+// four 16-byte groups of a row swizzled by (row / 4) % 4 (conflict-free
+// ds_read_b128 of the MFMA operands); the next block's raw bytes are loaded
+// into registers while the current block is computed, and two LDS stages
+// need one barrier per block.
+//
+// f16 conversions (exact):
+//  * code c -> f16(c - 1): v_perm picks the high byte from the table
+//    {0xBC, 0x00, 0x3C, 0x40} (f16 -1, 0, 1, 2 have zero low bytes), two more
+//    v_perm spread 4 high bytes into 4 halves;
+//  * q -> f16(q): v_perm builds the halves 0x6400 + (q + 128) (= 1024 + q +
+//    128), a packed f16 add of -1152 leaves q.
+constexpr int GF_BM = 128, GF_BN = 128, GF_THREADS = 512;
+constexpr int GF_STAGE_A = 4 * GF_BM * 64;          // bytes: [4 chunks][BM rows][64 B]
+constexpr int GF_STAGE_B = 4 * GF_BN * 64;
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void codes4_to_f16(uint32_t c4, uint32_t & lo, uint32_t & hi) {
+    const uint32_t hb = __builtin_amdgcn_perm(0u, 0x403C00BCu, c4);   // byte i = table[c_i]
+    lo = __builtin_amdgcn_perm(hb, 0u, 0x050C040Cu);                   // {0, hb0, 0, hb1}
+    hi = __builtin_amdgcn_perm(hb, 0u, 0x070C060Cu);                   // {0, hb2, 0, hb3}
+}
+
+__device__ __forceinline__ uint32_t sub1152_f16x2(uint32_t x) {
+    const v2h r = __builtin_bit_cast(v2h, x) + (v2h){(_Float16)-1152.0f, (_Float16)-1152.0f};
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+__device__ __forceinline__ void q4_to_f16(uint32_t q4, uint32_t & lo, uint32_t & hi) {
+    const uint32_t x = q4 ^ 0x80808080u;                               // q + 128 per byte
+    lo = sub1152_f16x2(__builtin_amdgcn_perm(x, 0x64646464u, 0x00050004u));
+    hi = sub1152_f16x2(__builtin_amdgcn_perm(x, 0x64646464u, 0x00070006u));
+}
+
+// Byte offset of the 16-byte group g of row r in a [rows][64 B] tile.  The
+// group is XOR-swizzled by ((r >> 1) ^ (r >> 2)) & 3 so that 16-byte accesses
+// of consecutive rows at one g hit distinct banks both with 32 banks (8
+// lanes per cycle) and with 64 banks (16 lanes per cycle).
+__device__ __forceinline__ int gf_swz(int r, int g) { return r * 64 + ((g ^ ((r >> 1) ^ (r >> 2))) & 3) * 16; }
+
+__global__ void __launch_bounds__(GF_THREADS)
+gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
+                float * __restrict__ Y, int n_out, int n_tok, int nb) {
+    __shared__ __attribute__((aligned(16))) uint8_t sA[2][GF_STAGE_A];
+    __shared__ __attribute__((aligned(16))) uint8_t sB[2][GF_STAGE_B];
+    __shared__ __attribute__((aligned(16))) float sDa[2][4][GF_BN];
+    __shared__ __attribute__((aligned(16))) float sDw[2][GF_BM];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int row0 = blockIdx.x * GF_BM, tok0 = blockIdx.y * GF_BN;
+    const int l16 = lane & 15, g = lane >> 4;
+    const size_t rs = (size_t)PQ2_BYTES * nb;                  // bytes per weight row
+    const size_t w_bytes = rs * (size_t)n_out;
+
+    // staging roles: A item (row ar, chunk ap), B item (token bt, chunk bp);
+    // LDS writes of a wave cover consecutive rows / tokens of one chunk
+    const int ar = tid & 127, ap = tid >> 7;                   // a wave stages 64 consecutive rows
+    const int bp = tid >> 7, bt = tid & 127;
+    const bool a_ok = row0 + ar < n_out;
+    const bool b_ok = tok0 + bt < n_tok;
+
+    // raw bytes of one block held in registers between its global load and
+    // its conversion into LDS; two sets, so a block's loads are issued two
+    // block-steps before they are consumed
+    struct Raw {
+        uint32_t a0, a1, a2, dw, sh;                           // A: 3-dword window, scale, shift
+        uint32_t q[9];                                         // B: one Q8_1 block
+    };
+    // byte offsets into W (kept as offsets so the loads stay global, not flat)
+    const size_t w_align = (uintptr_t)W & 3;
+    size_t a_off = (size_t)min(row0 + ar, n_out - 1) * rs + 2 + 8 * ap;   // chunk ap of block 0
+    const uint8_t * b_ptr = X + ((size_t)bp * n_tok + min(tok0 + bt, n_tok - 1)) * Q81_BYTES;
+    const size_t b_step = (size_t)4 * n_tok * Q81_BYTES;
+    int pf_block = 0;                                          // block the next prefetch reads
+    // Loads are unconditional (rows / tokens past the edge re-read the last
+    // one, the conversion zeroes them) so the compiler can count them: the
+    // wait before a conversion then leaves the younger block's loads in flight.
+    auto prefetch = [&](Raw & r) {                             // the next block in order (the last block again past the end)
+        // dword-aligned window (in absolute address terms) over the 8 code bytes
+        const size_t aa = ((a_off + w_align) & ~(size_t)3) - w_align;
+        r.sh = (uint32_t)((a_off + w_align) & 3);
+        r.a0 = *reinterpret_cast<const uint32_t *>(W + aa);
+        r.a1 = *reinterpret_cast<const uint32_t *>(W + aa + 4);
+        // the window may end 2 bytes past W when its last byte is the matrix's
+        // last: then read the dword ending at W's end and shift (flag in sh bit 2)
+        const bool tail = aa + 12 > w_bytes;
+        r.a2 = *reinterpret_cast<const uint32_t *>(W + (tail ? aa + 6 : aa + 8));
+        r.sh |= tail ? 4u : 0u;
+        r.dw = (uint32_t)*reinterpret_cast<const uint16_t *>(W + a_off - 2);
+        const uint32_t * xb = reinterpret_cast<const uint32_t *>(b_ptr);
+#pragma unroll
+        for (int k = 0; k < 9; ++k) r.q[k] = xb[k];
+        if (++pf_block < nb) {
+            a_off += PQ2_BYTES;
+            b_ptr += b_step;
+        }
+    };
+    auto commit = [&](const Raw & r, int st) {
+        const uint32_t sh = r.sh & 3u;
+        const uint32_t a2 = (r.sh & 4u) ? (r.a2 >> 16) : r.a2;
+        uint32_t w0 = __builtin_amdgcn_alignbyte(r.a1, r.a0, sh);
+        uint32_t w1 = __builtin_amdgcn_alignbyte(a2, r.a1, sh);
+        w0 = a_ok ? w0 : 0x55555555u;                           // code 1 -> weight 0
+        w1 = a_ok ? w1 : 0x55555555u;
+        uint8_t * a_dst = &sA[st][ap * GF_BM * 64];
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg) {
+            const uint32_t w = gg < 2 ? w0 : w1;
+            const int k0 = 2 * (gg & 1);                          // bit pair of position 8gg
+            uint32_t o0, o1, o2, o3;
+            codes4_to_f16((w >> (2 * k0)) & 0x03030303u, o0, o1);
+            codes4_to_f16((w >> (2 * k0 + 2)) & 0x03030303u, o2, o3);
+            *reinterpret_cast<v4u *>(a_dst + gf_swz(ar, gg)) = (v4u){o0, o1, o2, o3};
+        }
+        if (ap == 0) sDw[st][ar] = a_ok ? f16_bits_to_f32(r.dw) : 0.0f;
+        uint8_t * b_dst = &sB[st][bp * GF_BN * 64];
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg) {
+            uint32_t o0, o1, o2, o3;
+            q4_to_f16(b_ok ? r.q[1 + 2 * gg] : 0u, o0, o1);
+            q4_to_f16(b_ok ? r.q[2 + 2 * gg] : 0u, o2, o3);
+            *reinterpret_cast<v4u *>(b_dst + gf_swz(bt, gg)) = (v4u){o0, o1, o2, o3};
+        }
+        sDa[st][bp][bt] = b_ok ? f16_bits_to_f32(r.q[0] & 0xffffu) : 0.0f;
+    };
+
+    float acc[4][2][4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[mi][ni][i] = 0.0f;
+
+    Raw raw0, raw1;
+    prefetch(raw0);
+    prefetch(raw1);
+    commit(raw0, 0);
+    __syncthreads();
+    // step b: issue block b+2's loads into the set block b used, compute block
+    // b from LDS stage b&1, convert block b+1 (loaded a step earlier) into the
+    // other stage.  Every step issues and converts unconditionally (past the
+    // end it re-reads the last block and fills the unused stage), so the
+    // compiler's wait before the conversion leaves the younger loads in flight.
+    auto step = [&](int b, Raw & mine, Raw & next) {
+        const int st = b & 1;
+        prefetch(mine);
+        float inner[4][2][4];
+        // chunk p: 8 MFMAs, then their epilogue (the sched barriers keep the
+        // compiler from hoisting all 32 MFMAs of the block, which would hold
+        // 128 result registers)
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint8_t * a_src = &sA[st][p * GF_BM * 64];
+            const uint8_t * b_src = &sB[st][p * GF_BN * 64];
+            v8h A[4], Bf[2];
+            float da[2];
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+                A[mi] = *reinterpret_cast<const v8h *>(a_src + gf_swz(wm * 64 + 16 * mi + l16, g));
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                const int tt = wn * 32 + 16 * ni + l16;
+                Bf[ni] = *reinterpret_cast<const v8h *>(b_src + gf_swz(tt, g));
+                da[ni] = sDa[st][p][tt];
+            }
+            v4f S[4][2];
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+                    S[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mi], Bf[ni], (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        inner[mi][ni][i] = p == 0 ? da[ni] * S[mi][ni][i] : fmaf(da[ni], S[mi][ni][i], inner[mi][ni][i]);
+            // pin the chunk's epilogue here: without it the compiler sinks all
+            // the FMAs below the last MFMA and keeps 128 results live
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(inner[mi][ni][i]));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // per-row block scale: output rows 4g + i of each 16-row tile
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+            const v4f dw = *reinterpret_cast<const v4f *>(&sDw[st][wm * 64 + 16 * mi + 4 * g]);
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[mi][ni][i] = fmaf(dw[i], inner[mi][ni][i], acc[mi][ni][i]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        commit(next, st ^ 1);
+        __syncthreads();
+    };
+    // register sets alternate; an odd block count peels the first step
+    int b = 0;
+    if (nb & 1) {
+        step(0, raw0, raw1);
+        for (b = 1; b < nb; b += 2) {
+            step(b, raw1, raw0);
+            step(b + 1, raw0, raw1);
+        }
+    } else {
+        for (; b < nb; b += 2) {
+            step(b, raw0, raw1);
+            step(b + 1, raw1, raw0);
+        }
+    }
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+            const int tok = tok0 + wn * 32 + 16 * ni + l16;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = row0 + wm * 64 + 16 * mi + 4 * g + i;
+                if (row < n_out && tok < n_tok) Y[(size_t)row * n_tok + tok] = acc[mi][ni][i];
+            }
+        }
 }
 
 }  // namespace
@@ -457,7 +711,10 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
                            (int)n_out, (int)n_tok, nb);
         return (int)hipGetLastError();
     }
-    if ((nb & 1) || ((uintptr_t)W & 3u) != 0) {
+    if (env_int_gemm("BONSAI_GEMM_KERNEL", 0) == 0) {
+        dim3 grid((unsigned)cdiv(n_out, GF_BM), (unsigned)cdiv(n_tok, GF_BN));
+        hipLaunchKernelGGL(gemm_f16_kernel, grid, dim3(GF_THREADS), 0, st, w, x, Y, (int)n_out, (int)n_tok, nb);
+    } else if ((nb & 1) || ((uintptr_t)W & 3u) != 0) {
         dim3 grid((unsigned)cdiv(n_out, 64), (unsigned)cdiv(n_tok, 64));
         hipLaunchKernelGGL(gemm_mfma_kernel_u16, grid, dim3(256), 0, st, w, x, Y, (int)n_out, (int)n_tok, nb);
     } else if (n_tok <= 32) {
