@@ -526,7 +526,7 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
     // its conversion into LDS; two sets, so a block's loads are issued two
     // block-steps before they are consumed
     struct Raw {
-        uint32_t a0, a1, a2, dw, sh;                           // A: 3-dword window, scale, shift
+        uint32_t a0, a1, a2, dw, sh;                           // A: 3-dword window, scale, shift (bit 3: block in range)
         uint32_t q[9];                                         // B: one Q8_1 block
     };
     // byte offsets into W (kept as offsets so the loads stay global, not flat)
@@ -548,7 +548,7 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
         // last: then read the dword ending at W's end and shift (flag in sh bit 2)
         const bool tail = aa + 12 > w_bytes;
         r.a2 = *reinterpret_cast<const uint32_t *>(W + (tail ? aa + 6 : aa + 8));
-        r.sh |= tail ? 4u : 0u;
+        r.sh |= (tail ? 4u : 0u) | (pf_block < nb ? 8u : 0u);
         r.dw = (uint32_t)*reinterpret_cast<const uint16_t *>(W + a_off - 2);
         const uint32_t * xb = reinterpret_cast<const uint32_t *>(b_ptr);
 #pragma unroll
@@ -558,33 +558,37 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
             b_ptr += b_step;
         }
     };
+    // Conversion of one block's raw bytes into LDS stage st, in four parts
+    // (part q writes 16-byte group q of every A and B row) so that it can be
+    // interleaved with the four chunk steps of the current block.
+    uint32_t cw0, cw1;                                         // realigned code words
+    auto commit_part = [&](const Raw & r, int st, int q) {
+        if (q == 0) {
+            const uint32_t sh = r.sh & 3u;
+            const uint32_t a2 = (r.sh & 4u) ? (r.a2 >> 16) : r.a2;
+            cw0 = __builtin_amdgcn_alignbyte(r.a1, r.a0, sh);
+            cw1 = __builtin_amdgcn_alignbyte(a2, r.a1, sh);
+            cw0 = a_ok ? cw0 : 0x55555555u;                    // code 1 -> weight 0
+            cw1 = a_ok ? cw1 : 0x55555555u;
+            // a block past the end (the padding step of an odd block count) gets
+            // zero scales, so its products add exactly nothing
+            const bool live = (r.sh & 8u) != 0;
+            if (ap == 0) sDw[st][ar] = (a_ok && live) ? f16_bits_to_f32(r.dw) : 0.0f;
+            sDa[st][bp][bt] = (b_ok && live) ? f16_bits_to_f32(r.q[0] & 0xffffu) : 0.0f;
+        }
+        const uint32_t w = q < 2 ? cw0 : cw1;
+        const int k0 = 2 * (q & 1);                            // bit pair of position 8q
+        uint32_t o0, o1, o2, o3;
+        codes4_to_f16((w >> (2 * k0)) & 0x03030303u, o0, o1);
+        codes4_to_f16((w >> (2 * k0 + 2)) & 0x03030303u, o2, o3);
+        *reinterpret_cast<v4u *>(&sA[st][ap * GF_BM * 64] + gf_swz(ar, q)) = (v4u){o0, o1, o2, o3};
+        q4_to_f16(b_ok ? r.q[1 + 2 * q] : 0u, o0, o1);
+        q4_to_f16(b_ok ? r.q[2 + 2 * q] : 0u, o2, o3);
+        *reinterpret_cast<v4u *>(&sB[st][bp * GF_BN * 64] + gf_swz(bt, q)) = (v4u){o0, o1, o2, o3};
+    };
     auto commit = [&](const Raw & r, int st) {
-        const uint32_t sh = r.sh & 3u;
-        const uint32_t a2 = (r.sh & 4u) ? (r.a2 >> 16) : r.a2;
-        uint32_t w0 = __builtin_amdgcn_alignbyte(r.a1, r.a0, sh);
-        uint32_t w1 = __builtin_amdgcn_alignbyte(a2, r.a1, sh);
-        w0 = a_ok ? w0 : 0x55555555u;                           // code 1 -> weight 0
-        w1 = a_ok ? w1 : 0x55555555u;
-        uint8_t * a_dst = &sA[st][ap * GF_BM * 64];
 #pragma unroll
-        for (int gg = 0; gg < 4; ++gg) {
-            const uint32_t w = gg < 2 ? w0 : w1;
-            const int k0 = 2 * (gg & 1);                          // bit pair of position 8gg
-            uint32_t o0, o1, o2, o3;
-            codes4_to_f16((w >> (2 * k0)) & 0x03030303u, o0, o1);
-            codes4_to_f16((w >> (2 * k0 + 2)) & 0x03030303u, o2, o3);
-            *reinterpret_cast<v4u *>(a_dst + gf_swz(ar, gg)) = (v4u){o0, o1, o2, o3};
-        }
-        if (ap == 0) sDw[st][ar] = a_ok ? f16_bits_to_f32(r.dw) : 0.0f;
-        uint8_t * b_dst = &sB[st][bp * GF_BN * 64];
-#pragma unroll
-        for (int gg = 0; gg < 4; ++gg) {
-            uint32_t o0, o1, o2, o3;
-            q4_to_f16(b_ok ? r.q[1 + 2 * gg] : 0u, o0, o1);
-            q4_to_f16(b_ok ? r.q[2 + 2 * gg] : 0u, o2, o3);
-            *reinterpret_cast<v4u *>(b_dst + gf_swz(bt, gg)) = (v4u){o0, o1, o2, o3};
-        }
-        sDa[st][bp][bt] = b_ok ? f16_bits_to_f32(r.q[0] & 0xffffu) : 0.0f;
+        for (int q = 0; q < 4; ++q) commit_part(r, st, q);
     };
 
     float acc[4][2][4];
@@ -608,16 +612,16 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
     auto step = [&](int b, Raw & mine, Raw & next) {
         const int st = b & 1;
         prefetch(mine);
+        // chunk pipeline: the MFMAs of chunk p+1 are issued before the epilogue
+        // of chunk p, and a quarter of the next block's conversion follows each
+        // epilogue, so VALU work runs while the matrix core is busy
         float inner[4][2][4];
-        // chunk p: 8 MFMAs, then their epilogue (the sched barriers keep the
-        // compiler from hoisting all 32 MFMAs of the block, which would hold
-        // 128 result registers)
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
+        v4f S[2][4][2];
+        float da[2][2];
+        auto issue = [&](int p) {
             const uint8_t * a_src = &sA[st][p * GF_BM * 64];
             const uint8_t * b_src = &sB[st][p * GF_BN * 64];
             v8h A[4], Bf[2];
-            float da[2];
 #pragma unroll
             for (int mi = 0; mi < 4; ++mi)
                 A[mi] = *reinterpret_cast<const v8h *>(a_src + gf_swz(wm * 64 + 16 * mi + l16, g));
@@ -625,29 +629,40 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
             for (int ni = 0; ni < 2; ++ni) {
                 const int tt = wn * 32 + 16 * ni + l16;
                 Bf[ni] = *reinterpret_cast<const v8h *>(b_src + gf_swz(tt, g));
-                da[ni] = sDa[st][p][tt];
+                da[p & 1][ni] = sDa[st][p][tt];
             }
-            v4f S[4][2];
 #pragma unroll
             for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
                 for (int ni = 0; ni < 2; ++ni)
-                    S[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mi], Bf[ni], (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    S[p & 1][mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mi], Bf[ni], (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        };
+        auto epilogue = [&](int p) {
 #pragma unroll
             for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
                 for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        inner[mi][ni][i] = p == 0 ? da[ni] * S[mi][ni][i] : fmaf(da[ni], S[mi][ni][i], inner[mi][ni][i]);
+                        inner[mi][ni][i] = p == 0 ? da[0][ni] * S[0][mi][ni][i]
+                                                  : fmaf(da[p & 1][ni], S[p & 1][mi][ni][i], inner[mi][ni][i]);
             // pin the chunk's epilogue here: without it the compiler sinks all
-            // the FMAs below the last MFMA and keeps 128 results live
+            // the FMAs below the last MFMA and keeps every result live
 #pragma unroll
             for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
                 for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(inner[mi][ni][i]));
+        };
+        issue(0);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            if (p < 3) issue(p + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            epilogue(p);
+            __builtin_amdgcn_sched_barrier(0);
+            commit_part(next, st ^ 1, p);
             __builtin_amdgcn_sched_barrier(0);
         }
         // per-row block scale: output rows 4g + i of each 16-row tile
@@ -659,23 +674,13 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[mi][ni][i] = fmaf(dw[i], inner[mi][ni][i], acc[mi][ni][i]);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        commit(next, st ^ 1);
         __syncthreads();
     };
-    // register sets alternate; an odd block count peels the first step
-    int b = 0;
-    if (nb & 1) {
-        step(0, raw0, raw1);
-        for (b = 1; b < nb; b += 2) {
-            step(b, raw1, raw0);
-            step(b + 1, raw0, raw1);
-        }
-    } else {
-        for (; b < nb; b += 2) {
-            step(b, raw0, raw1);
-            step(b + 1, raw1, raw0);
-        }
+    // register sets alternate; an odd block count runs one padding step whose
+    // scales are zero
+    for (int b = 0; b < nb; b += 2) {
+        step(b, raw0, raw1);
+        step(b + 1, raw1, raw0);
     }
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
