@@ -36,6 +36,13 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
+// s_waitcnt vmcnt(N) with the other counters open (gfx9 encoding)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_sk() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
 __device__ __forceinline__ int codes_minus_one(uint32_t w, int k) {
     const uint32_t t = (w >> (2 * k)) & 0x03030303u;
     return (int)((t + 0x7f7f7f7fu) ^ 0x80808080u);
@@ -414,6 +421,203 @@ gemm_skinny_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Small batch, streamed (2 <= n_tok <= 16).  A workgroup owns R = 16 * RT
+// weight rows; its KS waves split K into contiguous ranges of pieces of 2
+// PQ2_0 blocks (nb even, nb >= 2 KS) and each wave streams its range through a private
+// LDS ring of two pieces: a piece is the R row segments of 68 bytes
+// (17 dwords, dword DMA) plus the 8 Q8_1 chunks of all n_tok tokens
+// (contiguous in the chunk-major X, dwordx4 DMA; NT >= n_tok bounds the
+// instruction count, and MFMA columns past n_tok repeat the last token and
+// are never stored).  All global reads are LDS DMA, so every wait is an
+// explicit vmcnt on this wave's own pieces.
+//
+// Per chunk: one v_mfma_i32_16x16x32_i8 per 16-row tile with A = the raw
+// codes (0..3) of 16 rows, B = the 32 permuted int8 of 16 token columns, and
+// the accumulator input C = -s of the lane's token, so the result is exactly
+// sum (code - 1) * q.  Lane l holds token l % 16 and rows 4(l/16) + i of the
+// tile: the per-token scale is lane-uniform (inner = da * S per chunk), the
+// per-row block scale is applied per block.  The KS partial sums meet in LDS.
+constexpr int SK_D = 2;                                   // ring depth (pieces)
+
+template <int RT, int KS, int NT>
+struct SkinnyCfg {
+    static constexpr int R = 16 * RT;
+    static constexpr int W_DW = R * 17;                   // weight dwords per piece
+    static constexpr int NIW = (W_DW + 63) / 64;
+    static constexpr int A_PC = 8 * NT * 9 / 4;           // 16-byte pieces of activation per piece (NT tokens)
+    static constexpr int NIA = (A_PC + 63) / 64;
+    static constexpr int PER = NIW + NIA;                 // DMA instructions per piece
+    static constexpr int W_BYTES = 64 * 4 * NIW;          // LDS bytes (every DMA lane has a slot)
+    static constexpr int A_BYTES = 64 * 16 * NIA;
+    static constexpr int SLOT = W_BYTES + A_BYTES;
+    static constexpr int LDS = KS * SK_D * SLOT;
+    static_assert(SK_D * PER < 64, "vmcnt range");
+    static_assert(LDS >= KS * R * 16 * 4, "reduction buffer fits in the ring");
+};
+
+// DMA of one piece: NIW dword instructions of weights, NIA dwordx4
+// instructions of activations.  (A free function: with the two DMA forms
+// inside a kernel lambda the host pass drops the kernel's host symbol.)
+template <int NIW, int NIA>
+__device__ __forceinline__ void small_issue(const uint8_t * wb, const uint32_t * woff,
+                                            const uint8_t * xb, const uint32_t * aoff,
+                                            uint8_t * dst, int w_bytes) {
+#pragma unroll
+    for (int k = 0; k < NIW; ++k)
+        __builtin_amdgcn_global_load_lds(wb + woff[k], (lds_void *)(dst + 256 * k), 4, 0, 0);
+#pragma unroll
+    for (int k = 0; k < NIA; ++k)
+        __builtin_amdgcn_global_load_lds(xb + aoff[k], (lds_void *)(dst + w_bytes + 1024 * k), 16, 0, 0);
+}
+
+template <int RT, int KS, int NT>
+__global__ void __launch_bounds__(64 * KS)
+gemm_small_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
+                  float * __restrict__ Y, int n_out, int n_tok, int nb) {
+    using C = SkinnyCfg<RT, KS, NT>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint8_t * ring = smem + (size_t)wave * SK_D * C::SLOT;
+    const int row0 = blockIdx.x * C::R;
+    const size_t rs = (size_t)PQ2_BYTES * nb;
+    // the nb / 2 pieces of a row are dealt to the KS waves in contiguous
+    // ranges that differ by at most one piece
+    const int np_all = nb / 2;
+    const int pbeg = wave * np_all / KS, pend = (wave + 1) * np_all / KS;
+    const int np = pend - pbeg;                             // pieces of this wave (>= 1)
+    const int blk0 = 2 * pbeg;
+
+    // per-lane DMA sources of one piece, as offsets from the piece's block
+    uint32_t woff[C::NIW];
+#pragma unroll
+    for (int k = 0; k < C::NIW; ++k) {
+        const int idx = min(64 * k + lane, C::W_DW - 1);   // lanes past the piece re-read its last dword
+        const int r = idx / 17, d = idx - 17 * r;
+        woff[k] = (uint32_t)(min(row0 + r, n_out - 1) * rs + 4 * d);
+    }
+    // the 8 chunks of a piece are 8 * n_tok contiguous Q8_1 blocks of the
+    // chunk-major X (288 * n_tok bytes, 16-byte aligned): dwordx4 DMA
+    const int a_pieces = 18 * n_tok;
+    uint32_t aoff[C::NIA];
+#pragma unroll
+    for (int k = 0; k < C::NIA; ++k) aoff[k] = 16u * (uint32_t)min(64 * k + lane, a_pieces - 1);
+    // piece j = blocks blk0 + 2j and blk0 + 2j + 1
+#define PQ2_SMALL_ISSUE(j, slot)                                                                   \
+    small_issue<C::NIW, C::NIA>(W + (size_t)PQ2_BYTES * (blk0 + 2 * (j)), woff,                      \
+                                X + (size_t)4 * (blk0 + 2 * (j)) * n_tok * Q81_BYTES, aoff,          \
+                                ring + (slot) * C::SLOT, C::W_BYTES)
+#pragma unroll
+    for (int i = 0; i < SK_D; ++i) PQ2_SMALL_ISSUE(min(i, np - 1), i);
+
+    const int l16 = lane & 15, g = lane >> 4;
+    const int h = g >> 1, pr = 2 * (g & 1);                // code word and first bit pair of K-group g
+    float acc[RT][4];
+#pragma unroll
+    for (int mt = 0; mt < RT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[mt][i] = 0.0f;
+
+    for (int j = 0; j < np; ++j) {
+        const int slot = j % SK_D;
+        if (j + 1 < np) wait_vmcnt_sk<C::PER>(); else wait_vmcnt_sk<0>();
+        __builtin_amdgcn_wave_barrier();
+        const uint8_t * wl = ring + slot * C::SLOT;
+        const uint8_t * al = wl + C::W_BYTES;
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb) {
+            float inner[RT][4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                // B: token column l16, K-group g of chunk 4bb + p; scale and -s of that token
+                const uint8_t * ab = al + ((4 * bb + p) * n_tok + min(l16, n_tok - 1)) * Q81_BYTES;
+                const uint32_t ds = *reinterpret_cast<const uint32_t *>(ab);
+                const uint32_t b0 = *reinterpret_cast<const uint32_t *>(ab + 4 + 8 * g);
+                const uint32_t b1 = *reinterpret_cast<const uint32_t *>(ab + 8 + 8 * g);
+                const int ns = -(int)(int16_t)(ds >> 16);
+                const float da = f16_bits_to_f32(ds & 0xffffu);
+                const long Bv = __builtin_bit_cast(long, (v2i){(int)b0, (int)b1});
+#pragma unroll
+                for (int mt = 0; mt < RT; ++mt) {
+                    // code word h of chunk p of block bb for row 16 mt + l16 (2-byte aligned
+                    // for bb = 0, dword aligned for bb = 1)
+                    const int off = (16 * mt + l16) * 68 + 34 * bb + 2 + 8 * p + 4 * h;
+                    uint32_t w;
+                    if (bb == 0) {
+                        const uint32_t lo = *reinterpret_cast<const uint32_t *>(wl + off - 2);
+                        const uint32_t hi = *reinterpret_cast<const uint32_t *>(wl + off + 2);
+                        w = __builtin_amdgcn_alignbyte(hi, lo, 2);
+                    } else {
+                        w = *reinterpret_cast<const uint32_t *>(wl + off);
+                    }
+                    const long Av = __builtin_bit_cast(long, (v2i){(int)((w >> (2 * pr)) & 0x03030303u),
+                                                                  (int)((w >> (2 * pr + 2)) & 0x03030303u)});
+                    const v4ia S = __builtin_amdgcn_mfma_i32_16x16x32_i8(Av, Bv, (v4ia){ns, ns, ns, ns}, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        inner[mt][i] = p == 0 ? da * (float)S[i] : fmaf(da, (float)S[i], inner[mt][i]);
+                }
+            }
+            // block scale of output rows 16 mt + 4g + i
+#pragma unroll
+            for (int mt = 0; mt < RT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t dwb = *reinterpret_cast<const uint16_t *>(wl + (16 * mt + 4 * g + i) * 68 + 34 * bb);
+                    acc[mt][i] = fmaf(f16_bits_to_f32(dwb), inner[mt][i], acc[mt][i]);
+                }
+        }
+        if (j + SK_D < np) {
+            __builtin_amdgcn_s_waitcnt(0xC07F);             // lgkmcnt(0): this slot's reads are done
+            __builtin_amdgcn_wave_barrier();
+            PQ2_SMALL_ISSUE(j + SK_D, slot);
+        }
+    }
+#undef PQ2_SMALL_ISSUE
+    // sum the KS partials of every (row, token) through LDS (the ring is free now)
+    __syncthreads();
+    float * red = reinterpret_cast<float *>(smem);            // [KS][R][16]
+#pragma unroll
+    for (int mt = 0; mt < RT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[(wave * C::R + 16 * mt + 4 * g + i) * 16 + l16] = acc[mt][i];
+    __syncthreads();
+    for (int e = threadIdx.x; e < C::R * 16; e += 64 * KS) {
+        const int rr = e >> 4, t = e & 15;
+        float v = 0.0f;
+#pragma unroll
+        for (int q = 0; q < KS; ++q) v += red[(q * C::R + rr) * 16 + t];
+        const int row = row0 + rr;
+        if (row < n_out && t < n_tok) Y[(size_t)row * n_tok + t] = v;
+    }
+}
+
+template <int RT, int KS, int NT>
+int launch_small_t(const uint8_t * W, const uint8_t * X, float * Y, int n_out, int n_tok, int nb,
+                   hipStream_t st) {
+    using C = SkinnyCfg<RT, KS, NT>;
+    auto kern = gemm_small_kernel<RT, KS, NT>;
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+        attr = true;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(n_out, C::R)), dim3(64 * KS), C::LDS, st, W, X, Y,
+                       n_out, n_tok, nb);
+    return (int)hipGetLastError();
+}
+
+template <int RT, int KS>
+int launch_small_nt(const uint8_t * W, const uint8_t * X, float * Y, int n_out, int n_tok, int nb,
+                    hipStream_t st) {
+    if (n_tok <= 2) return launch_small_t<RT, KS, 2>(W, X, Y, n_out, n_tok, nb, st);
+    if (n_tok <= 4) return launch_small_t<RT, KS, 4>(W, X, Y, n_out, n_tok, nb, st);
+    if (n_tok <= 8) return launch_small_t<RT, KS, 8>(W, X, Y, n_out, n_tok, nb, st);
+    return launch_small_t<RT, KS, 16>(W, X, Y, n_out, n_tok, nb, st);
+}
+
 template <int WM, int WN, int TM, int TN>
 void launch_gemm(const uint8_t * W, const uint8_t * X, float * Y, int n_out, int n_tok, int nb,
                  hipStream_t st) {
@@ -711,6 +915,25 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
     const uint8_t * x = (const uint8_t *)Xq;
     if (n_tok == 1) return bonsai_p40_gemv(W, Xq, Y, n_out, n_in, stream);   // chunk-major == token-major
     const size_t skinny_lds = (size_t)4 * 16 * PQ2_BYTES * (nb / 4) + 4096;
+    const int small_sel = env_int_gemm("BONSAI_GEMM_SMALL", 0);   // 0 streamed, 1 previous kernel
+    if (n_tok <= 16 && small_sel == 0 && nb % 2 == 0 && nb >= 8 && ((uintptr_t)W & 3u) == 0 &&
+        ((uintptr_t)Xq & 15u) == 0) {
+        switch (env_int_gemm("BONSAI_GEMM_SMALL_CFG", 0)) {
+            case 1: return launch_small_nt<1, 4>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
+            case 2: return launch_small_nt<2, 4>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
+            case 3: return launch_small_nt<4, 4>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
+            case 4: return launch_small_nt<1, 2>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
+            case 5: return launch_small_nt<2, 2>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
+            case 6: return launch_small_nt<4, 2>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
+            case 7: return launch_small_nt<1, 8>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
+            case 8: return launch_small_nt<1, 16>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
+            default: break;
+        }
+        // measured on MI355X: 16-row workgroups; K split 8 ways up to 8 tokens
+        // (more waves in flight), 4 ways for 9..16 tokens (the ring's LDS)
+        if (n_tok <= 8 && nb >= 16) return launch_small_nt<1, 8>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
+        return launch_small_nt<1, 4>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
+    }
     if (n_tok <= 16 && nb % 8 == 0 && ((uintptr_t)W & 3u) == 0 && skinny_lds <= (size_t)skinny_lds_limit()) {
         hipLaunchKernelGGL(gemm_skinny_kernel, dim3((unsigned)cdiv(n_out, 16)), dim3(256), skinny_lds, st, w, x, Y,
                            (int)n_out, (int)n_tok, nb);
