@@ -263,6 +263,10 @@ def main():
                     help="time Python launches one by one instead of replaying HIP graphs")
     ap.add_argument("--only-read", action="store_true",
                     help="stream-read probe over 23,750,272-byte buffers only (PMC calibration)")
+    ap.add_argument("--only-gemm", type=int, default=0, metavar="M",
+                    help="prefill GEMM 17408x5120 with M tokens only (profiling)")
+    ap.add_argument("--only-small", type=int, default=0, metavar="B",
+                    help="small-batch GEMM 17408x5120 with B tokens only (profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -284,6 +288,17 @@ def main():
         for _ in range(args.steps):
             z.zero_()              # writes 23,750,400 B: WRITE_SIZE calibration
         torch.cuda.synchronize()
+        return
+
+    if args.only_gemm or args.only_small:
+        m = args.only_gemm or args.only_small
+        ms = bench_gemv(N_FF, N_EMBD, args.steps, args.warmup, gen, n_tok=m)
+        if args.only_gemm:
+            tops = 2.0 * m * N_FF * N_EMBD / (ms * 1e-3) / 1e12
+            print(f"[bench] gemm 17408x5120 M={m}: {ms * 1e3:.1f} us  {tops:.1f} TOPS", file=sys.stderr, flush=True)
+        else:
+            gbs = gemv_bytes(N_FF, N_EMBD, m) / (ms * 1e-3) / 1e9
+            print(f"[bench] small batch 17408x5120 B={m}: {ms * 1e3:.2f} us  {gbs:.1f} GB/s", file=sys.stderr, flush=True)
         return
 
     # ---- headline: decode GEMV 17408x5120
@@ -343,7 +358,7 @@ def main():
                       file=sys.stderr, flush=True)
 
     traffic = load_traffic(os.path.join(ROOT, "profiles", "gemv_17408x5120_traffic.json"))
-    roof = {"bound": "hbm", "kernel": "gemv_nb_kernel<40> (bonsai_p40_gemv)",
+    roof = {"bound": "hbm", "kernel": "gemv_nb_kernel<40, 2, 4> (bonsai_p40_gemv)",
             "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "frac_of_achievable": round(gbs / read_gbs, 4),
