@@ -558,6 +558,13 @@ gemm_small_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X
                     for (int i = 0; i < 4; ++i)
                         inner[mt][i] = p == 0 ? da * (float)S[i] : fmaf(da, (float)S[i], inner[mt][i]);
                 }
+                // pin the chunk's epilogue here (otherwise every MFMA of the piece
+                // is hoisted into accumulator registers and converted at the end)
+#pragma unroll
+                for (int mt = 0; mt < RT; ++mt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(inner[mt][i]));
+                __builtin_amdgcn_sched_barrier(0);
             }
             // block scale of output rows 16 mt + 4g + i
 #pragma unroll

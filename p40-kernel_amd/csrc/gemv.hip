@@ -247,7 +247,10 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
     constexpr int ACT_BYTES = Q81_BYTES * P::NCH;
     constexpr int NA = (ACT_BYTES + 1023) / 1024;          // activation DMA instructions
     __shared__ __attribute__((aligned(16))) uint8_t act_lds[NA * 1024];
-    __shared__ __attribute__((aligned(16))) uint8_t ring_all[WAVES][D][P::LDSB];
+    // D units in flight per wave, D + 1 ring slots: the next unit is issued as
+    // soon as the current one has landed, before it is computed
+    constexpr int SL = D + 1;
+    __shared__ __attribute__((aligned(16))) uint8_t ring_all[WAVES][SL][P::LDSB];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     __builtin_assume(lane >= 0 && lane < 64);
@@ -346,12 +349,15 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
 
     int i = 0;
     do {
-        const int slot = i % D;
+        const int slot = i % SL;
         const int newer = min(D - 1, nu - 1 - i);
         if (newer >= 2) wait_vmcnt<2 * P::NPL>();
         else if (newer == 1) wait_vmcnt<P::NPL>();
         else wait_vmcnt<0>();
         __builtin_amdgcn_wave_barrier();
+        // unit i + D goes into the slot unit i - 1 used (its reads completed:
+        // lgkmcnt(0) at the end of the previous step)
+        if (i + D < nu) issue(gw + (i + D) * NW, (i + D) % SL);
         const uint8_t * ub = ring[slot];
         const int u = gw + i * NW;
 
@@ -390,12 +396,8 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
                 ykeep = (lane == i) ? t0 : ykeep;
             }
         }
-        // refill this slot with unit i + D once every lane's reads returned
-        if (i + D < nu) {
-            __builtin_amdgcn_s_waitcnt(0xC07F);    // lgkmcnt(0)
-            __builtin_amdgcn_wave_barrier();
-            issue(gw + (i + D) * NW, slot);
-        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);        // lgkmcnt(0): this slot's reads are done
+        __builtin_amdgcn_wave_barrier();
     } while (++i < nu);
     if (!DUMP) {
         const int row = (gw + (lane / P::G) * NW) * P::G + lane % P::G;
