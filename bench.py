@@ -152,6 +152,19 @@ def bench_stream_read(nbytes, steps, warmup, blocks=8192):
     return ms
 
 
+def bench_fwht_gemv(n_out, n_in, steps, warmup, gen):
+    """bonsai_p40_fwht_gemv: FWHT + Q8_1 of an fp32 activation and the GEMV in
+    one launch, over rotating weight copies."""
+    W0 = synth_weights(n_out, n_in, gen)
+    R = copies_for(W0.numel())
+    Ws = [W0] + [W0.clone() for _ in range(R - 1)]
+    x = torch.randn(n_in, generator=gen, device="cuda")
+    y = torch.empty(n_out, dtype=torch.float32, device="cuda")
+    ms = time_loop(lambda i: B.fwht_gemv(Ws[i % R], x, None, y, n_out, n_in), steps, warmup)
+    del Ws
+    return ms
+
+
 def bench_prepass(n, steps, warmup, gen):
     x = torch.randn(n, generator=gen, device="cuda")
     q = torch.empty(B.q8_bytes(n), dtype=torch.uint8, device="cuda")
@@ -187,9 +200,16 @@ def bench_ffn_chain(steps, warmup, gen):
     return ms, per + 0  # weight bytes per chain
 
 
-def bench_token_sweep(steps, warmup, gen):
-    """Config 2: 64 layers x (q, k, v, o, gate, up, down), each GEMV with its
-    own FWHT+Q8_1 pre-pass; 5.79 GB of distinct weights per token."""
+def bench_token_sweep(steps, warmup, gen, mode="separate"):
+    """Config 2: 64 layers x (q, k, v, o, gate, up, down) over 5.79 GB of
+    distinct weights per token, each GEMV fed by an FWHT+Q8_1 of its input.
+    mode "separate": a pre-pass launch before every GEMV (7 + 7 launches per
+    layer).  "fused": the rotation inside each GEMV launch
+    (bonsai_p40_fwht_gemv), except the 17408-wide down projection, whose
+    separate pre-pass is faster.  "grouped": as a model runs it -- q/k/v and
+    gate/up share their input, one grouped fused launch each
+    (bonsai_p40_fwht_gemv_group), o fused, down with its pre-pass (4 GEMV
+    launches + 1 pre-pass per layer)."""
     shapes = [(Q_DIM, N_EMBD), (KV_DIM, N_EMBD), (KV_DIM, N_EMBD), (N_EMBD, Q_DIM),
               (N_FF, N_EMBD), (N_FF, N_EMBD), (N_EMBD, N_FF)]
     proto = {s: synth_weights(s[0], s[1], gen) for s in set(shapes)}
@@ -199,11 +219,25 @@ def bench_token_sweep(steps, warmup, gen):
     ys = {n: torch.empty(n, device="cuda") for n in (Q_DIM, KV_DIM, N_EMBD, N_FF)}
     wbytes = sum(B.pq2_bytes(*s) for s in shapes) * N_LAYER
 
+    yk, yv, yg, yu = (torch.empty(n, device="cuda") for n in (KV_DIM, KV_DIM, N_FF, N_FF))
+
     def token(i):
         for L in layers:
+            if mode == "grouped":
+                Wq, Wk, Wv, Wo, Wg, Wu, Wd = L
+                B.fwht_gemv_group([Wq, Wk, Wv], xs[N_EMBD], None, [ys[Q_DIM], yk, yv],
+                                  [Q_DIM, KV_DIM, KV_DIM], N_EMBD)
+                B.fwht_gemv(Wo, xs[Q_DIM], None, ys[N_EMBD], N_EMBD, Q_DIM)
+                B.fwht_gemv_group([Wg, Wu], xs[N_EMBD], None, [yg, yu], [N_FF, N_FF], N_EMBD)
+                B.fwht_quant(xs[N_FF], None, qs[N_FF], N_FF)
+                B.gemv(Wd, qs[N_FF], ys[N_EMBD], N_EMBD, N_FF)
+                continue
             for (n_out, n_in), W in zip(shapes, L):
-                B.fwht_quant(xs[n_in], None, qs[n_in], n_in)
-                B.gemv(W, qs[n_in], ys[n_out], n_out, n_in)
+                if mode == "fused" and n_in != N_FF:
+                    B.fwht_gemv(W, xs[n_in], None, ys[n_out], n_out, n_in)
+                else:
+                    B.fwht_quant(xs[n_in], None, qs[n_in], n_in)
+                    B.gemv(W, qs[n_in], ys[n_out], n_out, n_in)
 
     ms = time_loop(token, steps, warmup, per_graph=1)
     del layers, proto
@@ -267,6 +301,8 @@ def main():
                     help="prefill GEMM 17408x5120 with M tokens only (profiling)")
     ap.add_argument("--only-small", type=int, default=0, metavar="B",
                     help="small-batch GEMM 17408x5120 with B tokens only (profiling)")
+    ap.add_argument("--only-fused", action="store_true",
+                    help="fused FWHT+Q8_1+GEMV 17408x5120 from fp32 only (profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -299,6 +335,11 @@ def main():
         else:
             gbs = gemv_bytes(N_FF, N_EMBD, m) / (ms * 1e-3) / 1e9
             print(f"[bench] small batch 17408x5120 B={m}: {ms * 1e3:.2f} us  {gbs:.1f} GB/s", file=sys.stderr, flush=True)
+        return
+
+    if args.only_fused:
+        ms = bench_fwht_gemv(N_FF, N_EMBD, args.steps, args.warmup, gen)
+        print(f"[bench] fwht_gemv 17408x5120: {ms * 1e3:.2f} us", file=sys.stderr, flush=True)
         return
 
     # ---- headline: decode GEMV 17408x5120
@@ -334,6 +375,13 @@ def main():
         for n in (N_EMBD, N_FF):
             m = bench_prepass(n, args.steps, args.warmup, gen)
             extra[f"fwht_quant_{n}_us"] = round(m * 1e3, 3)
+        for (n_out, n_in) in ((N_FF, N_EMBD), (N_EMBD, N_FF)):
+            m = bench_fwht_gemv(n_out, n_in, args.steps, args.warmup, gen)
+            extra[f"fwht_gemv_{n_out}x{n_in}"] = {
+                "us": round(m * 1e3, 3), "weight_GB/s": round(gemv_bytes(n_out, n_in) / (m * 1e-3) / 1e9, 1),
+                "note": "fp32 activation in: FWHT + Q8_1 + GEMV in one launch (bonsai_p40_fwht_gemv)"}
+            print(f"[bench] fwht_gemv {n_out}x{n_in}: {extra[f'fwht_gemv_{n_out}x{n_in}']}",
+                  file=sys.stderr, flush=True)
         m, wb = bench_ffn_chain(max(20, args.steps // 4), 5, gen)
         extra["ffn_chain_config1"] = {"us": round(m * 1e3, 2), "weight_GB/s": round(wb / (m * 1e-3) / 1e9, 1)}
         print(f"[bench] ffn chain: {extra['ffn_chain_config1']}", file=sys.stderr, flush=True)
@@ -342,6 +390,15 @@ def main():
                                         "weight_GB/s": round(wb / (m * 1e-3) / 1e9, 1),
                                         "weight_bytes": wb}
         print(f"[bench] token sweep: {extra['token_sweep_config2']}", file=sys.stderr, flush=True)
+        for mode, note in (("fused", "FWHT+Q8_1 inside each GEMV launch (down: separate pre-pass)"),
+                           ("grouped", "q/k/v and gate/up as grouped fused launches, o fused, "
+                                       "down with its pre-pass: 4 GEMV launches + 1 pre-pass per layer")):
+            m, wb = bench_token_sweep(5, 2, gen, mode=mode)
+            extra[f"token_sweep_config2_{mode}"] = {"ms_per_token": round(m, 3), "tok/s": round(1e3 / m, 2),
+                                                    "weight_GB/s": round(wb / (m * 1e-3) / 1e9, 1),
+                                                    "note": note}
+            print(f"[bench] token sweep {mode}: {extra[f'token_sweep_config2_{mode}']}", file=sys.stderr,
+                  flush=True)
         for bt in (2, 4, 8):
             for (n_out, n_in) in ((N_FF, N_EMBD), (N_EMBD, N_FF)):
                 m = bench_gemv(n_out, n_in, max(20, args.steps // 2), 10, gen, n_tok=bt)

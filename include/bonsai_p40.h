@@ -117,6 +117,37 @@ int bonsai_p40_quant_tokens(const float * X, const float * signs, void * Xq, int
 int bonsai_p40_swiglu_fwht_quant(const float * gate, const float * up, const float * signs,
                                  void * xq, int64_t n, bonsai_stream stream);
 
+// Fused decode GEMV from the fp32 activation: y = W . Q8_1(FWHT(signs .* x)),
+// one launch in place of bonsai_p40_fwht_quant followed by bonsai_p40_gemv
+// (the reference runs them as two kernels: elementwise_p40.cu:75-80 +
+// gemv_p40.cu:200-219).  Every workgroup rotates and quantises x into its own
+// LDS with the pre-pass's device code, so the Q8_1 bytes are the host's; on
+// the model widths (n_in/128 in {8, 40, 48, 80, 96, 136}) with 16-byte
+// aligned W, x and signs, y is bit-identical to the two-call sequence.  x is
+// not modified; signs may be NULL.  Errors: 1 if n_in <= 0, n_in % 1024 != 0,
+// x is NULL, or (other widths) the Q8_1 activation does not fit in LDS
+// (n_in > 130048); 0 (no-op) if n_out <= 0.
+int bonsai_p40_fwht_gemv(const void * W, const float * x, const float * signs, float * y,
+                         int64_t n_out, int64_t n_in, bonsai_stream stream);
+
+// Grouped decode GEMV: y[m] = W[m] . xq for the n_mat (1..4) matrices that
+// multiply one activation (q, k and v; gate and up), in one launch over the
+// concatenated rows (the reference launches one GEMV per matrix,
+// gemv_p40.cu:210-219).  W, y and n_out are host arrays of n_mat entries;
+// every W[m] has n_in columns.  y[m] is bit-identical to bonsai_p40_gemv on
+// W[m] alone.  Errors: as bonsai_p40_gemv, plus 1 if n_mat is outside 1..4,
+// an array is NULL or a matrix has more than 2^30 - 1 rows; matrices with
+// n_out[m] <= 0 are skipped (0 if all are).
+int bonsai_p40_gemv_group(const void * const * W, float * const * y, const int64_t * n_out, int n_mat,
+                          const void * xq, int64_t n_in, bonsai_stream stream);
+
+// Grouped form of bonsai_p40_fwht_gemv: y[m] = W[m] . Q8_1(FWHT(signs .* x)),
+// one rotation per workgroup for the whole group; y[m] is bit-identical to
+// bonsai_p40_fwht_gemv on W[m] alone.  Errors: as bonsai_p40_fwht_gemv and
+// bonsai_p40_gemv_group.
+int bonsai_p40_fwht_gemv_group(const void * const * W, float * const * y, const int64_t * n_out, int n_mat,
+                               const float * x, const float * signs, int64_t n_in, bonsai_stream stream);
+
 // Test hook: out[r * (n_in/32) + c] = the int32 chunk dot sum_k (code-1)*q of
 // row r, chunk c, computed by the same device code path as bonsai_p40_gemv
 // (the value of src/pq2_0.h:149-177 before scaling).  Errors as bonsai_p40_gemv.

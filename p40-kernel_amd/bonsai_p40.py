@@ -39,6 +39,9 @@ SIGNATURES = {
     "bonsai_p40_fwht_quant": [_F32P, _F32P, _V, _I64, _V],
     "bonsai_p40_quant_tokens": [_F32P, _F32P, _V, _I64, _I64, C.c_int, _V],
     "bonsai_p40_swiglu_fwht_quant": [_F32P, _F32P, _F32P, _V, _I64, _V],
+    "bonsai_p40_fwht_gemv": [_V, _F32P, _F32P, _F32P, _I64, _I64, _V],
+    "bonsai_p40_gemv_group": [_V, _V, _V, C.c_int, _V, _I64, _V],
+    "bonsai_p40_fwht_gemv_group": [_V, _V, _V, C.c_int, _F32P, _F32P, _I64, _V],
     "bonsai_p40_chunk_dots": [_V, _V, _V, _I64, _I64, _V],
     "bonsai_p40_stream_read": [_V, _I64, _V, C.c_int, _V],
 }
@@ -138,6 +141,38 @@ def quant_tokens(X, signs, Xq, n: int, n_tok: int, rotate: bool, stream=None) ->
 def swiglu_fwht_quant(gate, up, signs, xq, n: int, stream=None) -> None:
     _check("bonsai_p40_swiglu_fwht_quant",
            call("bonsai_p40_swiglu_fwht_quant", gate, up, signs, xq, n, stream=stream))
+
+
+def fwht_gemv(W, x, signs, y, n_out: int, n_in: int, stream=None) -> None:
+    _check("bonsai_p40_fwht_gemv",
+           call("bonsai_p40_fwht_gemv", W, x, signs, y, n_out, n_in, stream=stream))
+
+
+def _group_arrays(Ws, ys, n_outs):
+    n = len(Ws)
+    if not (len(ys) == n and len(n_outs) == n):
+        raise ValueError("Ws, ys and n_outs must have the same length")
+    Wa = (C.c_void_p * n)(*[_ptr(w) for w in Ws])
+    ya = (C.c_void_p * n)(*[_ptr(y) for y in ys])
+    na = (C.c_int64 * n)(*[int(r) for r in n_outs])
+    # keep the arrays alive for the call: the caller holds the returned tuple
+    return (Wa, ya, na), C.cast(Wa, C.c_void_p), C.cast(ya, C.c_void_p), C.cast(na, C.c_void_p), n
+
+
+def gemv_group(Ws, xq, ys, n_outs, n_in: int, stream=None) -> None:
+    """y_m = W_m . xq for up to 4 matrices sharing n_in, one launch."""
+    keep, Wp, yp, np_, n = _group_arrays(Ws, ys, n_outs)
+    rc = lib().bonsai_p40_gemv_group(Wp, yp, np_, n, _ptr(xq), n_in, _stream(stream))
+    del keep
+    _check("bonsai_p40_gemv_group", rc)
+
+
+def fwht_gemv_group(Ws, x, signs, ys, n_outs, n_in: int, stream=None) -> None:
+    """y_m = W_m . Q8_1(FWHT(signs .* x)) for up to 4 matrices, one launch."""
+    keep, Wp, yp, np_, n = _group_arrays(Ws, ys, n_outs)
+    rc = lib().bonsai_p40_fwht_gemv_group(Wp, yp, np_, n, _ptr(x), _ptr(signs), n_in, _stream(stream))
+    del keep
+    _check("bonsai_p40_fwht_gemv_group", rc)
 
 
 def chunk_dots(W, xq, out, n_out: int, n_in: int, stream=None) -> None:

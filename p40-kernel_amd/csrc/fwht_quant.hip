@@ -10,22 +10,17 @@
 // counterparts replaced: src/kernels/elementwise_p40.cu:17-41,75-80 and
 // src/kernels/gemv_p40.cu:168-208.
 //
-// One wave (64 lanes) owns one 1024-element block.  Lane l first holds the 16
-// consecutive elements 16l..16l+15 (layout A) and runs the stages h = 1..8 in
-// registers; two LDS transposes give layout B (reg index = element bits 4..7,
-// stages 16..128) and layout C (reg index = element bits 6..9, stages 256 and
-// 512); a third returns to layout A for the store.  Every stage is the same
-// a+b / a-b on the same operands in the same order h = 1, 2, ..., 512 as the
-// host loop, so the rotated values are bit-identical to fwht_blocks().  In
-// layout A a Q8_1 chunk is exactly a lane pair (l, l^1): the amax and the sum
-// need a single DPP exchange, and each lane writes its 16-element half already
-// transposed (activation word k = elements k, k+4, k+8, k+12).
+// One wave (64 lanes) owns one 1024-element block; the transform and the
+// quantiser are the register-resident device functions of fwht_device.h
+// (lane l holds the 16 consecutive elements of row fwht_row(l)), so the
+// rotated values are bit-identical to fwht_blocks() and the Q8_1 bytes to the
+// host quantiser.
 //
 // No floating-point contraction anywhere in this file: the host computes the
 // products x*id and x*sign as separately rounded fp32 multiplies.
 #pragma clang fp contract(off)
 
-#include "pq2_device.h"
+#include "fwht_device.h"
 #include "../../include/bonsai_p40.h"
 
 using namespace pq2;
@@ -42,75 +37,7 @@ enum : int {
     M_VEC = 64,       // 16-byte aligned fp32 pointers: dwordx4 loads/stores
 };
 
-template <int H>
-__device__ __forceinline__ void butterfly(float (&v)[16]) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        if (!(r & H)) {
-            const float a = v[r], b = v[r | H];
-            v[r] = a + b;
-            v[r | H] = a - b;
-        }
-    }
-}
-
-__device__ __forceinline__ void load16(const float * p, float (&v)[16], bool vec) {
-    if (vec) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float4 t = reinterpret_cast<const float4 *>(p)[k];
-            v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w;
-        }
-    } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = p[r];
-    }
-}
-
-__device__ __forceinline__ void store16(float * p, const float (&v)[16], bool vec) {
-    if (vec) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            reinterpret_cast<float4 *>(p)[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
-    } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) p[r] = v[r];
-    }
-}
-
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
-
-// Quantise the 32-element chunk held by the lane pair (l, l^1), 16 elements
-// per lane, and store it as one block_q8_1 at `blk` (4-byte aligned).
-// d = amax/127 (IEEE division), id = 1/d or 0, q = round-half-away(x*id)
-// clamped to +-127, s = sum q; d stored with the host's fp16 rounding.
-__device__ __forceinline__ void quant_pair_store(const float (&v)[16], uint8_t * blk, int half) {
-    float amax = 0.0f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) amax = fmaxf(amax, fabsf(v[r]));
-    amax = fmaxf(amax, dpp_mov<DPP_QUAD_XOR1>(amax));
-    const float d = amax / 127.0f;
-    const float id = d > 0.0f ? 1.0f / d : 0.0f;
-    int q[16];
-    int sum = 0;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const float prod = v[r] * id;
-        int t = (int)__builtin_roundf(prod);
-        t = t < -127 ? -127 : (t > 127 ? 127 : t);
-        q[r] = t;
-        sum += t;
-    }
-    sum += dpp_mov_i<DPP_QUAD_XOR1>(sum);
-    uint32_t * out = reinterpret_cast<uint32_t *>(blk);
-    if (half == 0) out[0] = f32_to_f16_away(d) | ((uint32_t)(sum & 0xffff) << 16);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        out[1 + 4 * half + k] = (uint32_t)(q[k] & 0xff) | ((uint32_t)(q[4 + k] & 0xff) << 8) |
-                                ((uint32_t)(q[8 + k] & 0xff) << 16) |
-                                ((uint32_t)(q[12 + k] & 0xff) << 24);
-    }
-}
 
 // Grid (n/1024, n_tok), 64 threads.  `x` (and `up` for SwiGLU) are [n_tok][n].
 template <int MODE>
@@ -118,12 +45,12 @@ __global__ void __launch_bounds__(64)
 rot_quant_kernel(const float * __restrict__ x, const float * __restrict__ up,
                  const float * __restrict__ signs, float * __restrict__ xout,
                  uint8_t * __restrict__ q, int n, int n_tok) {
-    __shared__ float s[17 * 64];
     const int l = threadIdx.x;
     const int blk = blockIdx.x;
     const int tok = blockIdx.y;
     const bool vec = (MODE & M_VEC) != 0;
-    const size_t base = (size_t)tok * n + (size_t)blk * HBLK + 16 * l;
+    const int row = fwht_row(l);
+    const size_t base = (size_t)tok * n + (size_t)blk * HBLK + 16 * row;
 
     float v[16];
     load16(x + base, v, vec);
@@ -135,42 +62,19 @@ rot_quant_kernel(const float * __restrict__ x, const float * __restrict__ up,
     }
     if (MODE & M_SIGNS) {
         float sg[16];
-        load16(signs + (size_t)blk * HBLK + 16 * l, sg, vec);
+        load16(signs + (size_t)blk * HBLK + 16 * row, sg, vec);
 #pragma unroll
         for (int r = 0; r < 16; ++r) v[r] *= sg[r];
     }
 
-    if (MODE & M_ROT) {
-        // layout A: element bits 0..3 in the register index
-        butterfly<1>(v); butterfly<2>(v); butterfly<4>(v); butterfly<8>(v);
-        // A -> B.  Element i lives at LDS word 17*(i>>4) + (i&15).
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[17 * l + r] = v[r];
-        __syncthreads();
-        const int lb = 17 * 16 * (l >> 4) + (l & 15);     // layout B: i = (l&15) | R<<4 | (l>>4)<<8
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = s[lb + 17 * r];
-        butterfly<1>(v); butterfly<2>(v); butterfly<4>(v); butterfly<8>(v);   // h = 16..128
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[lb + 17 * r] = v[r];
-        __syncthreads();
-        const int lc = 17 * (l >> 4) + (l & 15);           // layout C: i = l | R<<6
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = s[lc + 68 * r];
-        butterfly<4>(v); butterfly<8>(v);                   // h = 256, 512
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[lc + 68 * r] = v[r];
-        __syncthreads();
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = s[17 * l + r] * (1.0f / 32.0f);
-    }
+    if (MODE & M_ROT) fwht1024_regs(v, l);
 
     if (MODE & M_OUT_F32) store16(xout + base, v, vec);
     if (MODE & M_OUT_Q8) {
         const int nchunk = n / QK8;
-        const int c = blk * (HBLK / QK8) + (l >> 1);
+        const int c = blk * (HBLK / QK8) + (row >> 1);
         const size_t bidx = (MODE & M_CHUNK_MAJOR) ? (size_t)c * n_tok + tok : (size_t)tok * nchunk + c;
-        quant_pair_store(v, q + bidx * Q81_BYTES, l & 1);
+        quant_pair_store(v, q + bidx * Q81_BYTES, row & 1);
     }
 }
 

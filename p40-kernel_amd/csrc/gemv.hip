@@ -27,7 +27,7 @@
 //   fp32 row partials are reduced across the wave with DPP (quad_perm,
 //   row_half_mirror, row_mirror, row_bcast15/31) and lane 63 stores y.
 // Any other shape or alignment takes a simple wave-per-row kernel.
-#include "pq2_device.h"
+#include "fwht_device.h"
 #include "../../include/bonsai_p40.h"
 
 #include <stdlib.h>
@@ -232,20 +232,103 @@ __device__ __forceinline__ float wave_sum2_to_lanes31_63(float acc0, float acc1)
     return v;
 }
 
+// A group of up to MAX_GROUP matrices with the same n_in that multiply one
+// activation: unit u of the group's unit space is unit u - u0[m] of matrix m,
+// where m counts the starts u0[1..3] at or below u (entries past the last
+// matrix hold the total, so no unit maps there).  A matrix's units are
+// counted on their own (its last unit may hold fewer than G rows), so no
+// unit straddles two matrices.
+constexpr int MAX_GROUP = 4;
+struct MatGroup {
+    const uint8_t * W[MAX_GROUP];
+    float * y[MAX_GROUP];
+    int n_out[MAX_GROUP];
+    int u0[MAX_GROUP + 1];
+};
+
+// Per-unit view of a group, without branches: the starts are monotone, so
+// field F of the matrix owning unit u is F[0] + sum_k [u >= u0[k]] (F[k] -
+// F[k-1]), k = 1..3, with the differences formed once at kernel start (a
+// select between kernel-argument loads is turned into branches by the
+// compiler).  GROUP = false: one matrix, no selection at all.
+template <bool GROUP>
+struct GroupSel {
+    uint64_t w0, dw1, dw2, dw3;      // weight base and differences
+    uint64_t y0, dy1, dy2, dy3;      // output base and differences
+    int u1, u2, u3;                  // unit starts of matrices 1..3
+    int n0, dn1, dn2, dn3;           // row counts and differences
+
+    __device__ __forceinline__ explicit GroupSel(const MatGroup & mg) {
+        w0 = (uint64_t)mg.W[0];
+        y0 = (uint64_t)mg.y[0];
+        n0 = mg.n_out[0];
+        if constexpr (GROUP) {
+            dw1 = (uint64_t)mg.W[1] - w0; dw2 = (uint64_t)mg.W[2] - (uint64_t)mg.W[1];
+            dw3 = (uint64_t)mg.W[3] - (uint64_t)mg.W[2];
+            dy1 = (uint64_t)mg.y[1] - y0; dy2 = (uint64_t)mg.y[2] - (uint64_t)mg.y[1];
+            dy3 = (uint64_t)mg.y[3] - (uint64_t)mg.y[2];
+            u1 = mg.u0[1]; u2 = mg.u0[2]; u3 = mg.u0[3];
+            dn1 = mg.n_out[1] - n0; dn2 = mg.n_out[2] - mg.n_out[1]; dn3 = mg.n_out[3] - mg.n_out[2];
+        }
+    }
+    // fields of the matrix owning unit u; lu = u's index within it
+    __device__ __forceinline__ void at(int u, const uint8_t *& W, float *& y, int & n_out, int & lu) const {
+        if constexpr (!GROUP) {
+            W = reinterpret_cast<const uint8_t *>(w0);
+            y = reinterpret_cast<float *>(y0);
+            n_out = n0;
+            lu = u;
+        } else {
+            const uint64_t m1 = 0ull - (uint64_t)(u >= u1), m2 = 0ull - (uint64_t)(u >= u2),
+                           m3 = 0ull - (uint64_t)(u >= u3);
+            W = reinterpret_cast<const uint8_t *>(w0 + (dw1 & m1) + (dw2 & m2) + (dw3 & m3));
+            y = reinterpret_cast<float *>(y0 + (dy1 & m1) + (dy2 & m2) + (dy3 & m3));
+            const int k1 = (int)m1, k2 = (int)m2, k3 = (int)m3;
+            n_out = n0 + (dn1 & k1) + (dn2 & k2) + (dn3 & k3);
+            lu = u - ((u1 & k1) + ((u2 - u1) & k2) + ((u3 - u2) & k3));
+        }
+    }
+};
+
+// LDS staging of the fp32 activation (and signs) for the fused rotation:
+// block b at float 1024 b.  Function-scope LDS, so that only the kernels that
+// use it allocate it.
+template <int N>
+__device__ __forceinline__ float * rot_x_stage() {
+    __shared__ __attribute__((aligned(16))) float buf[N];
+    return buf;
+}
+template <int N>
+__device__ __forceinline__ float * rot_sign_stage() {
+    __shared__ __attribute__((aligned(16))) float buf[N];
+    return buf;
+}
+
 // Workgroup of WAVES waves.  Each wave owns up to `units_per_wave` units
 // (grid-strided) and a private ring of D unit buffers in LDS; the workgroup shares one
-// LDS copy of the Q8_1 activation.  Every global read is an LDS DMA
+// LDS copy of the Q8_1 activation.  Every weight read is an LDS DMA
 // (global_load_lds_dwordx4), so the only waits are the explicit vmcnt waits
 // below, and each unit is consumed as soon as its own bytes have landed.
-template <int NB, int D, int WAVES, bool DUMP>
+//
+// ROT = 0: `xin` is the permuted Q8_1 activation, DMA'd into LDS.
+// ROT = 1 (2 with signs): `xin` is the fp32 activation; the workgroup itself
+// computes Q8_1(FWHT(signs .* x)) into the same LDS block layout, wave w
+// taking the Hadamard blocks w, w + WAVES, ..., while its first weight units
+// are in flight.  x (and signs) reach LDS by DMA issued before any weight
+// DMA, so one explicit vmcnt wait covers them and leaves the weights
+// outstanding (a register load would make the compiler wait for everything
+// issued after it).
+template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, bool GROUP = false>
 __global__ void __launch_bounds__(64 * WAVES)
-gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
-               float * __restrict__ y, int32_t * __restrict__ dump, int n_out, int units_per_wave) {
+gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * __restrict__ signs,
+               int32_t * __restrict__ dump, int units_per_wave) {
     using P = NbSpec<NB>;
     static_assert(D >= 1 && D <= 3, "ring depth");
     static_assert(D * P::NPL < 64, "vmcnt range");
+    static_assert(ROT == 0 || P::NCH % 32 == 0, "the rotation needs whole 1024-element blocks");
     constexpr int ACT_BYTES = Q81_BYTES * P::NCH;
     constexpr int NA = (ACT_BYTES + 1023) / 1024;          // activation DMA instructions
+    constexpr int NHB = P::NCH / 32;                       // Hadamard blocks of the row
     __shared__ __attribute__((aligned(16))) uint8_t act_lds[NA * 1024];
     // D units in flight per wave, D + 1 ring slots: the next unit is issued as
     // soon as the current one has landed, before it is computed
@@ -255,8 +338,8 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     __builtin_assume(lane >= 0 && lane < 64);
     uint8_t (*ring)[P::LDSB] = ring_all[wave];
-    const int n_units = (n_out + P::G - 1) / P::G;
-    const int n_full = n_out / P::G;                        // units with all G rows present
+    const int n_units = mg.u0[MAX_GROUP];
+    const GroupSel<GROUP> gs(mg);
     // units are dealt to waves grid-strided: wave gw owns units gw, gw + NW,
     // gw + 2 NW, ...  Every issue round then reads one contiguous stretch of
     // W across the whole grid; a contiguous per-wave span of 3 units
@@ -268,10 +351,31 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
     const int NW = gridDim.x * WAVES;
     const int nu = gw < n_units ? min(units_per_wave, (n_units - 1 - gw) / NW + 1) : 0;
 
-    // 1. activation share of this wave (instructions k = wave, wave + WAVES, ...)
-    for (int k = wave; k < NA; k += WAVES) {
-        const int off = min(16 * (64 * k + lane), ACT_BYTES - 16);
-        __builtin_amdgcn_global_load_lds(xq + off, (lds_void *)(&act_lds[1024 * k]), 16, 0, 0);
+    // 1. activation: ROT = 0 -- this wave's share of the Q8_1 DMA
+    //    (instructions k = wave, wave + WAVES, ...); ROT > 0 -- the fp32
+    //    blocks (and signs) of this wave into its staging areas
+    if constexpr (ROT == 0) {
+        const uint8_t * xq = static_cast<const uint8_t *>(xin);
+        for (int k = wave; k < NA; k += WAVES) {
+            const int off = min(16 * (64 * k + lane), ACT_BYTES - 16);
+            __builtin_amdgcn_global_load_lds(xq + off, (lds_void *)(&act_lds[1024 * k]), 16, 0, 0);
+        }
+    } else {
+        const float * x = static_cast<const float *>(xin);
+        float * xst = rot_x_stage<NHB * HBLK>();
+        for (int b = wave; b < NHB; b += WAVES) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                __builtin_amdgcn_global_load_lds(x + HBLK * b + 256 * j + 4 * lane,
+                                                 (lds_void *)(xst + HBLK * b + 256 * j), 16, 0, 0);
+            if constexpr (ROT == 2) {
+                float * sst = rot_sign_stage<NHB * HBLK>();
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    __builtin_amdgcn_global_load_lds(signs + HBLK * b + 256 * j + 4 * lane,
+                                                     (lds_void *)(sst + HBLK * b + 256 * j), 16, 0, 0);
+            }
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -282,16 +386,20 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
     uint32_t poff[P::NPL];
 #pragma unroll
     for (int k = 0; k < P::NPL; ++k) poff[k] = 16u * (uint32_t)min(lane + 64 * k, P::NPIECE - 1);
-    const size_t last_piece = (size_t)n_out * PQ2_BYTES * NB / 16 - 1;
     auto issue = [&](int uu, int slot) {
-        const uint8_t * base = W + (size_t)uu * P::UB;
-        const bool full = uu < n_full;
+        const uint8_t * Wm;
+        float * ym;
+        int n_out_m, lu;
+        gs.at(uu, Wm, ym, n_out_m, lu);
+        const uint8_t * base = Wm + (size_t)lu * P::UB;
+        const bool full = lu < n_out_m / P::G;              // all G rows present
+        const size_t last_piece = (size_t)n_out_m * PQ2_BYTES * NB / 16 - 1;
 #pragma unroll
         for (int k = 0; k < P::NPL; ++k) {
             const uint8_t * src = base + poff[k];
             if (!full) {
-                size_t p = (size_t)uu * (P::UB / 16) + poff[k] / 16;
-                src = W + 16 * (p < last_piece ? p : last_piece);
+                size_t p = (size_t)lu * (P::UB / 16) + poff[k] / 16;
+                src = Wm + 16 * (p < last_piece ? p : last_piece);
             }
             // nt: weights stream through L2 without displacing the activation
             __builtin_amdgcn_global_load_lds(src, (lds_void *)(&ring[slot][1024 * k]), 16, 0, CPOL_NT);
@@ -309,12 +417,38 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // 3. own activation share landed (all unit DMAs are younger), then the
-    //    workgroup barrier makes every share visible
-    if (nu > 0) wait_vmcnt<D * P::NPL>();
-    else wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();
-    if (nu <= 0) return;
+    if constexpr (ROT == 0) {
+        // 3. own activation share landed (all unit DMAs are younger), then the
+        //    workgroup barrier makes every share visible
+        if (nu > 0) wait_vmcnt<D * P::NPL>();
+        else wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        if (nu <= 0) return;
+    } else {
+        // 3. own staged blocks landed (all unit DMAs are younger); rotate and
+        //    quantise them into the LDS activation (chunk c of block b at byte
+        //    36 (32 b + c)), then the workgroup barrier makes every block visible
+        if (nu > 0) wait_vmcnt<D * P::NPL>();
+        else wait_vmcnt<0>();
+        const int row = fwht_row(lane);
+        for (int b = wave; b < NHB; b += WAVES) {
+            const float * xb = rot_x_stage<NHB * HBLK>() + HBLK * b + 16 * row;
+            float v[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) v[r] = xb[r];
+            if constexpr (ROT == 2) {
+#pragma clang fp contract(off)
+                const float * sb = rot_sign_stage<NHB * HBLK>() + HBLK * b + 16 * row;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) v[r] *= sb[r];
+            }
+            fwht1024_regs(v, lane);
+            quant_pair_store(v, &act_lds[Q81_BYTES * (32 * b + (row >> 1))], row & 1);
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);        // lgkmcnt(0): this wave's LDS stores are done
+        __builtin_amdgcn_s_barrier();
+        if (nu <= 0) return;
+    }
 
     // the lane's chunk of slot j is the same in every unit: its activation
     // nibble planes, scale and -s bias stay in registers
@@ -373,7 +507,7 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
             if (DUMP) {
                 const int v = 64 * j + lane;
                 const int row = u * P::G + (second ? 1 : 0);
-                if (v < P::G * P::NCH && row < n_out)
+                if (v < P::G * P::NCH && row < mg.n_out[0])     // single matrix
                     dump[(size_t)row * P::NCH + (second ? v - P::NCH : v)] = s;
             } else {
                 const float t = da[j] * (float)s;
@@ -399,9 +533,13 @@ gemv_nb_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ xq,
         __builtin_amdgcn_s_waitcnt(0xC07F);        // lgkmcnt(0): this slot's reads are done
         __builtin_amdgcn_wave_barrier();
     } while (++i < nu);
-    if (!DUMP) {
-        const int row = (gw + (lane / P::G) * NW) * P::G + lane % P::G;
-        if (lane < nu * P::G && row < n_out) y[row] = ykeep;
+    if (!DUMP && lane < nu * P::G) {
+        const uint8_t * Wm;
+        float * ym;
+        int n_out_m, lu;
+        gs.at(gw + (lane / P::G) * NW, Wm, ym, n_out_m, lu);
+        const int row = lu * P::G + lane % P::G;
+        if (row < n_out_m) ym[row] = ykeep;
     }
 }
 
@@ -518,15 +656,43 @@ int default_wg_per_cu(int nb, int64_t w_bytes) {
     return w_bytes >= (16 << 20) ? 3 : 2;
 }
 
-template <int NB, int D, int WAVES, bool DUMP>
-int launch_nb_t(const uint8_t * W, const uint8_t * xq, float * y, int32_t * dump, int n_out,
-                hipStream_t st) {
+// LDS bytes of one gemv_nb_kernel workgroup (all static allocations)
+template <int NB, int D, int WAVES, int ROT>
+constexpr int nb_lds_bytes() {
     using P = NbSpec<NB>;
-    const int n_units = (n_out + P::G - 1) / P::G;
+    constexpr int act = (Q81_BYTES * P::NCH + 1023) / 1024 * 1024;
+    constexpr int ring = WAVES * (D + 1) * P::LDSB;
+    constexpr int nhb = P::NCH / 32;
+    constexpr int stage = (ROT ? nhb * HBLK * 4 : 0) + (ROT == 2 ? nhb * HBLK * 4 : 0);
+    return act + ring + stage;
+}
+
+constexpr int LDS_PER_CU = 160 * 1024;
+
+// Unit starts of a group; false if the group's unit count overflows int.
+template <int G>
+bool group_units(MatGroup & mg, int n_mat) {
+    int64_t u = 0;
+    for (int m = 0; m < MAX_GROUP; ++m) {
+        mg.u0[m] = (int)u;
+        if (m < n_mat) u += (mg.n_out[m] + G - 1) / G;
+        else { mg.W[m] = nullptr; mg.y[m] = nullptr; mg.n_out[m] = 0; }
+    }
+    for (int m = n_mat; m <= MAX_GROUP; ++m) mg.u0[m] = (int)u;
+    return u < 0x40000000;
+}
+
+template <int NB, int D, int WAVES, bool DUMP, int ROT = 0>
+int launch_nb_t(MatGroup mg, int n_mat, const void * xin, const float * signs, int32_t * dump,
+                int per_cu, hipStream_t st) {
+    using P = NbSpec<NB>;
+    constexpr int lds = nb_lds_bytes<NB, D, WAVES, ROT>();
+    static_assert(lds <= LDS_PER_CU, "workgroup LDS");
+    if (!group_units<P::G>(mg, n_mat)) return 1;
+    const int n_units = mg.u0[MAX_GROUP];
     // a whole number of workgroups per CU (the dispatcher then places exactly
     // that many on every CU), fewer for small matrices
-    int per_cu = env_int("BONSAI_GEMV_WG_PER_CU", 0);
-    if (per_cu <= 0) per_cu = default_wg_per_cu(NB, (int64_t)n_out * PQ2_BYTES * NB);
+    if (per_cu > LDS_PER_CU / lds) per_cu = LDS_PER_CU / lds;
     int blocks = per_cu * cu_count();
     const int max_blocks = (n_units + WAVES - 1) / WAVES;
     if (blocks > max_blocks) blocks = max_blocks;
@@ -536,51 +702,214 @@ int launch_nb_t(const uint8_t * W, const uint8_t * xq, float * y, int32_t * dump
         upw = 64 / P::G;
         blocks = (n_units + upw * WAVES - 1) / (upw * WAVES);
     }
-    hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, DUMP>), dim3(blocks), dim3(64 * WAVES), 0, st, W, xq,
-                       y, dump, n_out, upw);
+    if (n_mat > 1)
+        hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, DUMP, ROT, true>), dim3(blocks), dim3(64 * WAVES), 0,
+                           st, mg, xin, signs, dump, upw);
+    else
+        hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, DUMP, ROT, false>), dim3(blocks), dim3(64 * WAVES), 0,
+                           st, mg, xin, signs, dump, upw);
     return (int)hipGetLastError();
 }
 
-template <int NB, bool DUMP>
-int launch_nb(const uint8_t * W, const uint8_t * xq, float * y, int32_t * dump, int n_out,
-              hipStream_t st) {
-    // 4-wave workgroups with two unit buffers per wave measured best at every
-    // model width (deeper rings queue more bytes ahead of the activation)
-    return launch_nb_t<NB, 2, 4, DUMP>(W, xq, y, dump, n_out, st);
+int64_t group_weight_bytes(const MatGroup & mg, int n_mat, int nb) {
+    int64_t b = 0;
+    for (int m = 0; m < n_mat; ++m) b += (int64_t)mg.n_out[m] * PQ2_BYTES * nb;
+    return b;
 }
 
-template <bool DUMP>
-int gemv_dispatch(const void * W, const void * xq, float * y, int32_t * dump, int64_t n_out,
-                  int64_t n_in, hipStream_t st) {
-    const uint8_t * w = static_cast<const uint8_t *>(W);
-    const uint8_t * x = static_cast<const uint8_t *>(xq);
-    if (n_out > 0x7fffffff || n_in / QK_PQ2 > (1 << 24)) return 1;
-    const bool w_al16 = ((uintptr_t)w & 15u) == 0;
-    const int kernel_sel = env_int("BONSAI_GEMV_KERNEL", 0);   // 0 auto, 1 stream, 2 generic
-    if (w_al16 && ((uintptr_t)x & 15u) == 0 && kernel_sel == 0) {
+template <int NB, bool DUMP>
+int launch_nb(const MatGroup & mg, int n_mat, const uint8_t * xq, int32_t * dump, hipStream_t st) {
+    // 4-wave workgroups with two unit buffers per wave measured best at every
+    // model width (deeper rings queue more bytes ahead of the activation)
+    int per_cu = env_int("BONSAI_GEMV_WG_PER_CU", 0);
+    if (per_cu <= 0) per_cu = default_wg_per_cu(NB, group_weight_bytes(mg, n_mat, NB));
+    return launch_nb_t<NB, 2, 4, DUMP>(mg, n_mat, xq, nullptr, dump, per_cu, st);
+}
+
+// Fused rotation: every workgroup rotates the whole activation, so the
+// fused kernel wants few, wide workgroups: 8 waves and one workgroup per CU
+// where the LDS allows (measured on MI355X: 7.7 us at 17408x5120, 5.5-5.6 us
+// at 6144x5120 and 5120x6144, against 9.9 / 7.0 / 6.8 us for the pre-pass
+// plus the GEMV; two workgroups per CU: 6.9 us at 5120x6144), else 4 waves
+// with D = 2 or D = 1.  Returns -1 when no shape fits the LDS of a workgroup.
+template <int NB, int ROT>
+int launch_nb_rot(const MatGroup & mg, int n_mat, const float * x, const float * signs, hipStream_t st) {
+    const int waves = env_int("BONSAI_FGEMV_WAVES", 8);
+    int per_cu = env_int("BONSAI_GEMV_WG_PER_CU", 0);
+    if (per_cu <= 0) per_cu = 1;
+    if constexpr (nb_lds_bytes<NB, 2, 8, ROT>() <= LDS_PER_CU) {
+        if (waves == 8) return launch_nb_t<NB, 2, 8, false, ROT>(mg, n_mat, x, signs, nullptr, per_cu, st);
+    }
+    if constexpr (nb_lds_bytes<NB, 2, 4, ROT>() <= LDS_PER_CU)
+        return launch_nb_t<NB, 2, 4, false, ROT>(mg, n_mat, x, signs, nullptr, per_cu, st);
+    else if constexpr (nb_lds_bytes<NB, 1, 4, ROT>() <= LDS_PER_CU)
+        return launch_nb_t<NB, 1, 4, false, ROT>(mg, n_mat, x, signs, nullptr, per_cu, st);
+    else
+        return -1;
+}
+
+// Generic fused path (any n_in % 1024 == 0 whose Q8_1 activation fits in
+// LDS): every workgroup rotates and quantises the whole activation into LDS
+// (one Hadamard block per wave at a time), then each wave computes one row
+// with the lane-strided chunk walk of gemv_rowwave_kernel.
+__global__ void __launch_bounds__(GV_THREADS)
+gemv_rot_generic_kernel(const uint8_t * __restrict__ W, const float * __restrict__ x,
+                        const float * __restrict__ signs, float * __restrict__ y, int n_out, int nb,
+                        bool vec) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nchunk = 4 * nb;
+    uint8_t * act = smem;
+    const int xrow = fwht_row(lane);
+    for (int b = wave; b < nchunk / 32; b += GV_WAVES) {
+        float v[16];
+        load16(x + (size_t)HBLK * b + 16 * xrow, v, vec);
+        if (signs != nullptr) {
+#pragma clang fp contract(off)
+            float sg[16];
+            load16(signs + (size_t)HBLK * b + 16 * xrow, sg, vec);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) v[r] *= sg[r];
+        }
+        fwht1024_regs(v, lane);
+        quant_pair_store(v, act + (size_t)Q81_BYTES * (32 * b + (xrow >> 1)), xrow & 1);
+    }
+    __syncthreads();
+    const int row = blockIdx.x * GV_WAVES + wave;
+    if (row >= n_out) return;
+    const uint8_t * wr = W + (size_t)row * PQ2_BYTES * nb;
+    float acc = 0.0f;
+    for (int c = lane; c < nchunk; c += 64) {
+        const uint8_t * blk = wr + (size_t)PQ2_BYTES * (c >> 2);
+        const uint16_t * qp = reinterpret_cast<const uint16_t *>(blk + 2 + 8 * (c & 3));
+        const uint32_t w0 = (uint32_t)qp[0] | ((uint32_t)qp[1] << 16);
+        const uint32_t w1 = (uint32_t)qp[2] | ((uint32_t)qp[3] << 16);
+        const uint32_t * ab = reinterpret_cast<const uint32_t *>(act + (size_t)Q81_BYTES * c);
+        const uint32_t ds = ab[0];
+        const int a[8] = {(int)ab[1], (int)ab[2], (int)ab[3], (int)ab[4],
+                          (int)ab[5], (int)ab[6], (int)ab[7], (int)ab[8]};
+        const int s = chunk_dot_i32(w0, w1, a, -(int)(int16_t)(ds >> 16));
+        const float dw = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(blk));
+        acc += dw * (f16_bits_to_f32(ds & 0xffffu) * (float)s);
+    }
+    acc = wave_sum_to_lane63(acc);
+    if (lane == 63) y[row] = acc;
+}
+
+size_t rot_generic_lds(int64_t n_in) { return (size_t)(n_in / QK8) * Q81_BYTES; }
+
+bool group_w_aligned(const MatGroup & mg, int n_mat) {
+    for (int m = 0; m < n_mat; ++m)
+        if (((uintptr_t)mg.W[m] & 15u) != 0) return false;
+    return true;
+}
+
+// Fused FWHT + Q8_1 + GEMV of a group: one streaming launch on the model
+// widths, else one generic fused launch per matrix.
+int fwht_gemv_group_dispatch(const MatGroup & mg, int n_mat, const float * x, const float * signs,
+                             int64_t n_in, hipStream_t st) {
+    const bool al = group_w_aligned(mg, n_mat) && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)signs & 15u) == 0;
+    if (al && env_int("BONSAI_GEMV_KERNEL", 0) == 0) {
+        int rc = -1;
+#define PQ2_ROT_CASE(N)                                                                         \
+    case N: rc = signs ? launch_nb_rot<N, 2>(mg, n_mat, x, signs, st)                           \
+                       : launch_nb_rot<N, 1>(mg, n_mat, x, signs, st); break;
         switch (n_in / QK_PQ2) {
-            case 8: return launch_nb<8, DUMP>(w, x, y, dump, (int)n_out, st);
-            case 40: return launch_nb<40, DUMP>(w, x, y, dump, (int)n_out, st);
-            case 48: return launch_nb<48, DUMP>(w, x, y, dump, (int)n_out, st);
-            case 80: return launch_nb<80, DUMP>(w, x, y, dump, (int)n_out, st);
-            case 96: return launch_nb<96, DUMP>(w, x, y, dump, (int)n_out, st);
-            case 136: return launch_nb<136, DUMP>(w, x, y, dump, (int)n_out, st);
+            PQ2_ROT_CASE(8) PQ2_ROT_CASE(40) PQ2_ROT_CASE(48) PQ2_ROT_CASE(80) PQ2_ROT_CASE(96)
+            PQ2_ROT_CASE(136)
             default: break;
         }
+#undef PQ2_ROT_CASE
+        if (rc >= 0) return rc;
     }
+    const size_t lds = rot_generic_lds(n_in);
+    if (lds > (size_t)max_lds_per_block()) return 1;
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_rot_generic_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, max_lds_per_block());
+        attr_set = true;
+    }
+    const bool vec = ((uintptr_t)x & 15u) == 0 && ((uintptr_t)signs & 15u) == 0;
+    for (int m = 0; m < n_mat; ++m) {
+        if (mg.n_out[m] <= 0) continue;
+        const unsigned blocks = (unsigned)((mg.n_out[m] + GV_WAVES - 1) / GV_WAVES);
+        hipLaunchKernelGGL(gemv_rot_generic_kernel, dim3(blocks), dim3(GV_THREADS), lds, st, mg.W[m], x,
+                           signs, mg.y[m], mg.n_out[m], (int)(n_in / QK_PQ2), vec);
+        const int rc = (int)hipGetLastError();
+        if (rc != 0) return rc;
+    }
+    return 0;
+}
+
+// One matrix on the widths without a specialised kernel: the runtime-shaped
+// streaming kernel, or the generic wave-per-row kernel.
+template <bool DUMP>
+int gemv_other(const uint8_t * w, const uint8_t * x, float * y, int32_t * dump, int n_out, int64_t n_in,
+               int kernel_sel, hipStream_t st) {
     const StreamGeom g = stream_geom(n_in);
     const bool fast = (n_in % HBLK == 0) && (((uintptr_t)w & 15u) == 0) && g.npl <= MAX_NPL &&
                       g.lds_bytes <= (size_t)max_lds_per_block() &&
                       kernel_sel != 2;
     if (fast) {
-        const int rc = (g.G == 1) ? launch_stream_g<1, DUMP>(w, x, y, dump, (int)n_out, g, st)
-                                  : launch_stream_g<2, DUMP>(w, x, y, dump, (int)n_out, g, st);
+        const int rc = (g.G == 1) ? launch_stream_g<1, DUMP>(w, x, y, dump, n_out, g, st)
+                                  : launch_stream_g<2, DUMP>(w, x, y, dump, n_out, g, st);
         if (rc >= 0) return rc;
     }
     const unsigned blocks = (unsigned)((n_out + GV_WAVES - 1) / GV_WAVES);
     hipLaunchKernelGGL(gemv_rowwave_kernel<DUMP>, dim3(blocks), dim3(GV_THREADS), 0, st, w, x, y,
-                       dump, (int)n_out, g.nb);
+                       dump, n_out, g.nb);
     return (int)hipGetLastError();
+}
+
+template <bool DUMP>
+int gemv_group_dispatch(const MatGroup & mg, int n_mat, const void * xq, int32_t * dump, int64_t n_in,
+                        hipStream_t st) {
+    const uint8_t * x = static_cast<const uint8_t *>(xq);
+    const int kernel_sel = env_int("BONSAI_GEMV_KERNEL", 0);   // 0 auto, 1 stream, 2 generic
+    if (group_w_aligned(mg, n_mat) && ((uintptr_t)x & 15u) == 0 && kernel_sel == 0) {
+        switch (n_in / QK_PQ2) {
+            case 8: return launch_nb<8, DUMP>(mg, n_mat, x, dump, st);
+            case 40: return launch_nb<40, DUMP>(mg, n_mat, x, dump, st);
+            case 48: return launch_nb<48, DUMP>(mg, n_mat, x, dump, st);
+            case 80: return launch_nb<80, DUMP>(mg, n_mat, x, dump, st);
+            case 96: return launch_nb<96, DUMP>(mg, n_mat, x, dump, st);
+            case 136: return launch_nb<136, DUMP>(mg, n_mat, x, dump, st);
+            default: break;
+        }
+    }
+    for (int m = 0; m < n_mat; ++m) {
+        if (mg.n_out[m] <= 0) continue;
+        const int rc = gemv_other<DUMP>(mg.W[m], x, mg.y[m], dump, mg.n_out[m], n_in, kernel_sel, st);
+        if (rc != 0) return rc;
+    }
+    return 0;
+}
+
+// Host arrays of a group -> MatGroup.  Returns 1 on bad arguments, 0 with
+// *n_rows = 0 for an empty group, else 0.
+int make_group(MatGroup & mg, const void * const * W, float * const * y, const int64_t * n_out, int n_mat,
+               int64_t * n_rows) {
+    *n_rows = 0;
+    if (n_mat < 1 || n_mat > MAX_GROUP || W == nullptr || y == nullptr || n_out == nullptr) return 1;
+    for (int m = 0; m < MAX_GROUP; ++m) {
+        const int64_t r = m < n_mat ? n_out[m] : 0;
+        if (r > 0x3fffffff) return 1;
+        mg.W[m] = m < n_mat ? static_cast<const uint8_t *>(W[m]) : nullptr;
+        mg.y[m] = m < n_mat ? y[m] : nullptr;
+        mg.n_out[m] = r > 0 ? (int)r : 0;
+        *n_rows += mg.n_out[m];
+    }
+    return 0;
+}
+
+MatGroup single_group(const void * W, float * y, int64_t n_out) {
+    MatGroup mg{};
+    mg.W[0] = static_cast<const uint8_t *>(W);
+    mg.y[0] = y;
+    mg.n_out[0] = (int)n_out;
+    return mg;
 }
 
 }  // namespace
@@ -591,14 +920,46 @@ int bonsai_p40_gemv(const void * W, const void * xq, float * y, int64_t n_out, i
                     bonsai_stream stream) {
     if (n_in <= 0 || n_in % QK_PQ2 != 0 || ((uintptr_t)xq & 3u) != 0) return 1;
     if (n_out <= 0) return 0;
-    return gemv_dispatch<false>(W, xq, y, nullptr, n_out, n_in, (hipStream_t)stream);
+    if (n_out > 0x3fffffff || n_in / QK_PQ2 > (1 << 24)) return 1;
+    return gemv_group_dispatch<false>(single_group(W, y, n_out), 1, xq, nullptr, n_in, (hipStream_t)stream);
+}
+
+int bonsai_p40_gemv_group(const void * const * W, float * const * y, const int64_t * n_out, int n_mat,
+                          const void * xq, int64_t n_in, bonsai_stream stream) {
+    if (n_in <= 0 || n_in % QK_PQ2 != 0 || ((uintptr_t)xq & 3u) != 0) return 1;
+    if (n_in / QK_PQ2 > (1 << 24)) return 1;
+    MatGroup mg;
+    int64_t rows = 0;
+    if (make_group(mg, W, y, n_out, n_mat, &rows) != 0) return 1;
+    if (rows == 0) return 0;
+    return gemv_group_dispatch<false>(mg, n_mat, xq, nullptr, n_in, (hipStream_t)stream);
+}
+
+int bonsai_p40_fwht_gemv(const void * W, const float * x, const float * signs, float * y,
+                         int64_t n_out, int64_t n_in, bonsai_stream stream) {
+    if (n_in <= 0 || n_in % HBLK != 0 || x == nullptr) return 1;
+    if (n_out <= 0) return 0;
+    if (n_out > 0x3fffffff || n_in / QK_PQ2 > (1 << 24)) return 1;
+    return fwht_gemv_group_dispatch(single_group(W, y, n_out), 1, x, signs, n_in, (hipStream_t)stream);
+}
+
+int bonsai_p40_fwht_gemv_group(const void * const * W, float * const * y, const int64_t * n_out, int n_mat,
+                               const float * x, const float * signs, int64_t n_in, bonsai_stream stream) {
+    if (n_in <= 0 || n_in % HBLK != 0 || x == nullptr) return 1;
+    if (n_in / QK_PQ2 > (1 << 24)) return 1;
+    MatGroup mg;
+    int64_t rows = 0;
+    if (make_group(mg, W, y, n_out, n_mat, &rows) != 0) return 1;
+    if (rows == 0) return 0;
+    return fwht_gemv_group_dispatch(mg, n_mat, x, signs, n_in, (hipStream_t)stream);
 }
 
 int bonsai_p40_chunk_dots(const void * W, const void * xq, int32_t * out, int64_t n_out,
                           int64_t n_in, bonsai_stream stream) {
     if (n_in <= 0 || n_in % QK_PQ2 != 0 || ((uintptr_t)xq & 3u) != 0) return 1;
     if (n_out <= 0) return 0;
-    return gemv_dispatch<true>(W, xq, nullptr, out, n_out, n_in, (hipStream_t)stream);
+    if (n_out > 0x3fffffff || n_in / QK_PQ2 > (1 << 24)) return 1;
+    return gemv_group_dispatch<true>(single_group(W, nullptr, n_out), 1, xq, out, n_in, (hipStream_t)stream);
 }
 
 }  // extern "C"

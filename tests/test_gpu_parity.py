@@ -222,6 +222,108 @@ def test_gemv_code3_and_extremes():
     np.testing.assert_array_equal(host(out), O.chunk_dots(W, xq, n_out, n_in))
 
 
+# ------------------------------------------------------- fused FWHT + GEMV
+ROT_WIDTHS = (8, 40, 48, 80, 96, 136)     # n_in / 128 of the streaming kernel
+
+
+@pytest.mark.parametrize("n_out,n_in,signed", [
+    (17408, 5120, False), (6144, 5120, True), (1024, 5120, False), (5120, 6144, True),
+    (5120, 17408, False), (5120, 17408, True), (17407, 5120, True), (333, 1024, False),
+    (97, 10240, True), (100, 12288, True), (77, 2048, True), (64, 3072, False), (1, 5120, False)])
+def test_fwht_gemv(n_out, n_in, signed):
+    case(f"fwht_gemv {n_out}x{n_in} signed={signed}")
+    W = O.gen_weights(1600 + n_out + n_in, n_out, n_in)
+    x = O.gen_normal(1601 + n_in, n_in)
+    s = np.where(O.gen_normal(1602 + n_in, n_in) > 0, 1.0, -1.0).astype(np.float32) if signed else None
+    Wd, xd = dev(W), dev(x)
+    sd = None if s is None else dev(s)
+    y = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+    B.fwht_gemv(Wd, xd, sd, y, n_out, n_in)
+    got = host(y)
+    xq_ref = O.quantize_q8_1(O.fwht(x, s), True)
+    assert np.all(np.isfinite(got))
+    assert normwise(got, O.gemv(W, xq_ref, n_out, n_in, nthreads=16)) <= TOL
+    np.testing.assert_array_equal(bits(host(xd)), bits(x))          # x is not modified
+    # the separate pre-pass + GEMV: same Q8_1 bytes, and on the streaming
+    # widths the same kernel arithmetic, so the same bits
+    q = torch.zeros(n_in // 32 * 36, dtype=torch.uint8, device="cuda")
+    B.fwht_quant(xd, sd, q, n_in)
+    y2 = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+    B.gemv(Wd, q, y2, n_out, n_in)
+    if n_in // 128 in ROT_WIDTHS and not (signed and n_in == 17408):
+        np.testing.assert_array_equal(bits(got), bits(host(y2)))
+    # a second call in a row gives the same bits (no state)
+    B.fwht_gemv(Wd, xd, sd, y, n_out, n_in)
+    np.testing.assert_array_equal(bits(host(y)), bits(got))
+
+
+GROUPS = [
+    (5120, (6144, 1024, 1024)),               # q, k, v
+    (5120, (17408, 17408)),                   # gate, up
+    (5120, (17407, 3, 0, 1001)),              # ragged: partial 2-row units, an empty matrix
+    (6144, (5120, 7)),
+    (17408, (5120, 100, 33)),
+    (2048, (64, 300)),                        # no streaming kernel: one launch per matrix
+]
+
+
+@pytest.mark.parametrize("n_in,n_outs", GROUPS)
+def test_gemv_group(n_in, n_outs):
+    case(f"gemv_group n_in={n_in} n_outs={n_outs}")
+    Ws = [O.gen_weights(1800 + m + n_in, max(r, 1), n_in) for m, r in enumerate(n_outs)]
+    xq = O.quantize_q8_1(O.fwht(O.gen_normal(1810 + n_in, n_in)), True)
+    Wd = [dev(W) for W in Ws]
+    xd = dev(xq)
+    ys = [torch.full((max(r, 1),), float("nan"), dtype=torch.float32, device="cuda") for r in n_outs]
+    B.gemv_group(Wd, xd, ys, n_outs, n_in)
+    for W, Wdm, y, r in zip(Ws, Wd, ys, n_outs):
+        got = host(y)
+        if r == 0:
+            assert np.isnan(got).all()        # skipped: untouched
+            continue
+        assert normwise(got, O.gemv(W, xq, r, n_in, nthreads=16)) <= TOL
+        y1 = torch.full((r,), float("nan"), dtype=torch.float32, device="cuda")
+        B.gemv(Wdm, xd, y1, r, n_in)
+        np.testing.assert_array_equal(bits(got), bits(host(y1)))
+
+
+@pytest.mark.parametrize("n_in,n_outs", GROUPS)
+@pytest.mark.parametrize("signed", [False, True])
+def test_fwht_gemv_group(n_in, n_outs, signed):
+    case(f"fwht_gemv_group n_in={n_in} n_outs={n_outs} signed={signed}")
+    Ws = [O.gen_weights(1900 + m + n_in, max(r, 1), n_in) for m, r in enumerate(n_outs)]
+    x = O.gen_normal(1910 + n_in, n_in)
+    s = np.where(O.gen_normal(1911 + n_in, n_in) > 0, 1.0, -1.0).astype(np.float32) if signed else None
+    xq = O.quantize_q8_1(O.fwht(x, s), True)
+    Wd = [dev(W) for W in Ws]
+    xd = dev(x)
+    sd = None if s is None else dev(s)
+    ys = [torch.full((max(r, 1),), float("nan"), dtype=torch.float32, device="cuda") for r in n_outs]
+    B.fwht_gemv_group(Wd, xd, sd, ys, n_outs, n_in)
+    for W, Wdm, y, r in zip(Ws, Wd, ys, n_outs):
+        got = host(y)
+        if r == 0:
+            assert np.isnan(got).all()
+            continue
+        assert normwise(got, O.gemv(W, xq, r, n_in, nthreads=16)) <= TOL
+        y1 = torch.full((r,), float("nan"), dtype=torch.float32, device="cuda")
+        B.fwht_gemv(Wdm, xd, sd, y1, r, n_in)
+        np.testing.assert_array_equal(bits(got), bits(host(y1)))
+
+
+@pytest.mark.parametrize("x_offset", [4, 8])
+def test_fwht_gemv_unaligned_x(x_offset):
+    case(f"fwht_gemv unaligned x offset {x_offset}")
+    n_out, n_in = 300, 5120
+    W = O.gen_weights(1700, n_out, n_in)
+    x = O.gen_normal(1701, n_in)
+    buf, xp = offset_copy(x.view(np.uint8), x_offset)
+    y = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+    B.fwht_gemv(dev(W), xp, None, y, n_out, n_in)
+    ref = O.gemv(W, O.quantize_q8_1(O.fwht(x), True), n_out, n_in)
+    assert normwise(host(y), ref) <= TOL
+
+
 # ------------------------------------------------------------------ repack
 @pytest.mark.parametrize("n_out,n_in", [(8, 5120), (33, 17408), (5, 1024), (16, 6144)])
 def test_repack_bytes_and_gemv_repack(n_out, n_in):

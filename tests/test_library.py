@@ -56,12 +56,33 @@ NULL = None
     ("bonsai_p40_quant_tokens", (NULL, NULL, NULL, 1000, 2, 1), 1),
     ("bonsai_p40_quant_tokens", (NULL, NULL, NULL, 1024, 0, 1), 1),
     ("bonsai_p40_swiglu_fwht_quant", (NULL, NULL, NULL, NULL, 100), 1),
+    ("bonsai_p40_fwht_gemv", (NULL, 16, NULL, NULL, 16, 1000), 1),    # n_in % 1024
+    ("bonsai_p40_fwht_gemv", (NULL, NULL, NULL, NULL, 16, 1024), 1),  # x NULL
+    ("bonsai_p40_fwht_gemv", (NULL, 16, NULL, NULL, 0, 1024), 0),     # empty no-op
+    ("bonsai_p40_gemv_group", (NULL, NULL, NULL, 1, NULL, 128), 1),   # NULL arrays
+    ("bonsai_p40_fwht_gemv_group", (NULL, NULL, NULL, 1, 16, NULL, 1024), 1),
     ("bonsai_p40_rmsnorm", (NULL, NULL, NULL, 0, 64, C.c_float(1e-6)), 0),
     ("bonsai_p40_rmsnorm", (NULL, NULL, NULL, 4, 0, C.c_float(1e-6)), 1),
 ])
 def test_argument_checks(name, args, rc):
     fn = getattr(B.lib(), name)
     assert fn(*args, None) == rc
+
+
+def test_group_argument_checks():
+    L = B.lib()
+    W = (C.c_void_p * 5)(*([16] * 5))
+    y = (C.c_void_p * 5)(*([16] * 5))
+    n = (C.c_int64 * 5)(*([0] * 5))
+    Wp, yp, np_ = (C.cast(a, C.c_void_p) for a in (W, y, n))
+    assert L.bonsai_p40_gemv_group(Wp, yp, np_, 0, None, 128, None) == 1         # n_mat < 1
+    assert L.bonsai_p40_gemv_group(Wp, yp, np_, 5, None, 128, None) == 1         # n_mat > 4
+    assert L.bonsai_p40_gemv_group(Wp, yp, np_, 3, None, 128, None) == 0         # all empty
+    assert L.bonsai_p40_gemv_group(Wp, yp, np_, 3, None, 100, None) == 1         # n_in % 128
+    assert L.bonsai_p40_fwht_gemv_group(Wp, yp, np_, 2, 16, None, 1024, None) == 0
+    assert L.bonsai_p40_fwht_gemv_group(Wp, yp, np_, 2, 16, None, 2000, None) == 1
+    n[1] = 1 << 30
+    assert L.bonsai_p40_gemv_group(Wp, yp, np_, 2, None, 128, None) == 1         # too many rows
 
 
 def test_out_of_scope_entries_report_not_implemented():
