@@ -908,6 +908,12 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
 
 }  // namespace
 
+namespace pq2 {
+// gemv.hip: 2..4 tokens on the streaming GEMV kernel; -1 if not applicable
+int gemv_small_batch(const void * W, const void * Xq, float * Y, int64_t n_out, int64_t n_in,
+                     int64_t n_tok, bonsai_stream stream);
+}
+
 extern "C" {
 
 int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, int64_t n_in,
@@ -921,6 +927,10 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
     const uint8_t * w = (const uint8_t *)W;
     const uint8_t * x = (const uint8_t *)Xq;
     if (n_tok == 1) return bonsai_p40_gemv(W, Xq, Y, n_out, n_in, stream);   // chunk-major == token-major
+    if (n_tok <= 4) {
+        const int rc = pq2::gemv_small_batch(W, Xq, Y, n_out, n_in, n_tok, stream);
+        if (rc >= 0) return rc;
+    }
     const size_t skinny_lds = (size_t)4 * 16 * PQ2_BYTES * (nb / 4) + 4096;
     const int small_sel = env_int_gemm("BONSAI_GEMM_SMALL", 0);   // 0 streamed, 1 previous kernel
     if (n_tok <= 16 && small_sel == 0 && nb % 2 == 0 && nb >= 8 && ((uintptr_t)W & 3u) == 0 &&

@@ -186,10 +186,12 @@ gemv_stream_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ 
 //   scale 1/16 folded into the activation scale.
 // G = 1 when 4*nb % 64 == 0; otherwise G = 2 if that needs <= 8 slots, else
 // G = 1 with a half-empty last slot whose idle lanes carry zero activations.
-template <int NB>
+// With NT >= 3 tokens G = 1 (fewer slots, so the per-token activation planes
+// fit in registers).
+template <int NB, int NT = 1>
 struct NbSpec {
     static constexpr int NCH = 4 * NB;
-    static constexpr int G = (NCH % 64 == 0) ? 1 : ((2 * NCH / 64) <= 8 ? 2 : 1);
+    static constexpr int G = (NCH % 64 == 0 || NT >= 3) ? 1 : ((2 * NCH / 64) <= 8 ? 2 : 1);
     static constexpr int S = (G * NCH + 63) / 64;
     static constexpr int UB = G * PQ2_BYTES * NB;
     static constexpr int NPIECE = UB / 16;
@@ -245,6 +247,14 @@ struct MatGroup {
     int n_out[MAX_GROUP];
     int u0[MAX_GROUP + 1];
 };
+
+MatGroup single_group(const void * W, float * y, int64_t n_out) {
+    MatGroup mg{};
+    mg.W[0] = static_cast<const uint8_t *>(W);
+    mg.y[0] = y;
+    mg.n_out[0] = (int)n_out;
+    return mg;
+}
 
 // Per-unit view of a group, without branches: the starts are monotone, so
 // field F of the matrix owning unit u is F[0] + sum_k [u >= u0[k]] (F[k] -
@@ -318,15 +328,22 @@ __device__ __forceinline__ float * rot_sign_stage() {
 // DMA, so one explicit vmcnt wait covers them and leaves the weights
 // outstanding (a register load would make the compiler wait for everything
 // issued after it).
-template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, bool GROUP = false>
+//
+// NT > 1 (small batch, n_tok <= NT tokens): xin is the chunk-major Q8_1 of
+// the tokens (block (c, t) at c n_tok + t, the GEMM's X layout); every lane
+// keeps the nibble planes of its chunk for each token, so a unit's code words
+// are extracted once and dotted against NT activations.  Tokens past n_tok
+// have zero planes; y is [n_out][n_tok].
+template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, bool GROUP = false, int NT = 1>
 __global__ void __launch_bounds__(64 * WAVES)
 gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * __restrict__ signs,
-               int32_t * __restrict__ dump, int units_per_wave) {
-    using P = NbSpec<NB>;
+               int32_t * __restrict__ dump, int units_per_wave, int n_tok) {
+    using P = NbSpec<NB, NT>;
+    static_assert(NT == 1 || (!DUMP && ROT == 0 && !GROUP), "small batch: plain GEMV only");
     static_assert(D >= 1 && D <= 3, "ring depth");
     static_assert(D * P::NPL < 64, "vmcnt range");
     static_assert(ROT == 0 || P::NCH % 32 == 0, "the rotation needs whole 1024-element blocks");
-    constexpr int ACT_BYTES = Q81_BYTES * P::NCH;
+    constexpr int ACT_BYTES = Q81_BYTES * P::NCH * NT;
     constexpr int NA = (ACT_BYTES + 1023) / 1024;          // activation DMA instructions
     constexpr int NHB = P::NCH / 32;                       // Hadamard blocks of the row
     __shared__ __attribute__((aligned(16))) uint8_t act_lds[NA * 1024];
@@ -356,8 +373,10 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
     //    blocks (and signs) of this wave into its staging areas
     if constexpr (ROT == 0) {
         const uint8_t * xq = static_cast<const uint8_t *>(xin);
-        for (int k = wave; k < NA; k += WAVES) {
-            const int off = min(16 * (64 * k + lane), ACT_BYTES - 16);
+        const int act_bytes = NT == 1 ? ACT_BYTES : Q81_BYTES * P::NCH * n_tok;
+        const int na = NT == 1 ? NA : (act_bytes + 1023) / 1024;
+        for (int k = wave; k < na; k += WAVES) {
+            const int off = min(16 * (64 * k + lane), act_bytes - 16);
             __builtin_amdgcn_global_load_lds(xq + off, (lds_void *)(&act_lds[1024 * k]), 16, 0, 0);
         }
     } else {
@@ -452,23 +471,28 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
 
     // the lane's chunk of slot j is the same in every unit: its activation
     // nibble planes, scale and -s bias stay in registers
-    uint32_t ah[P::S][4], al[P::S][4];
-    float da[P::S];
-    int bias[P::S];
+    uint32_t ah[NT][P::S][4], al[NT][P::S][4];
+    float da[NT][P::S];
+    int bias[NT][P::S];
 #pragma unroll
     for (int j = 0; j < P::S; ++j) {
         const int v = 64 * j + lane;
         const bool valid = v < P::G * P::NCH;
         int c = v >= P::NCH ? v - P::NCH : v;
         c = valid ? c : 0;
-        const uint32_t * a = reinterpret_cast<const uint32_t *>(&act_lds[Q81_BYTES * c]);
-        const uint32_t ds = a[0];
-        uint32_t aw[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) aw[k] = valid ? a[1 + k] : 0u;
-        nib_planes(aw, ah[j], al[j]);
-        da[j] = valid ? f16_bits_to_f32(ds & 0xffffu) : 0.0f;
-        bias[j] = valid ? -(int)(int16_t)(ds >> 16) : 0;
+        for (int t = 0; t < NT; ++t) {
+            const bool tv = valid && (NT == 1 || t < n_tok);
+            const int blk = NT == 1 ? c : (tv ? c * n_tok + t : 0);
+            const uint32_t * a = reinterpret_cast<const uint32_t *>(&act_lds[Q81_BYTES * blk]);
+            const uint32_t ds = a[0];
+            uint32_t aw[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) aw[k] = tv ? a[1 + k] : 0u;
+            nib_planes(aw, ah[t][j], al[t][j]);
+            da[t][j] = tv ? f16_bits_to_f32(ds & 0xffffu) : 0.0f;
+            bias[t][j] = tv ? -(int)(int16_t)(ds >> 16) : 0;
+        }
     }
 
     // code bytes of the lane's chunk: 8 bytes at a 2-byte aligned LDS offset,
@@ -479,7 +503,7 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
     const int sh = cw & 3;
     const int cw_al = cw - sh;
     const int dwo = PQ2_BYTES * (lane >> 2);
-    float ykeep = 0.0f;                       // lane G*i + r keeps row r of unit i
+    float ykeep = 0.0f;                       // lane (G i + r) NT + t keeps row r, token t of unit i
 
     int i = 0;
     do {
@@ -495,51 +519,64 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         const uint8_t * ub = ring[slot];
         const int u = gw + i * NW;
 
-        float acc0 = 0.0f, acc1 = 0.0f;
+        float acc0[NT], acc1[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc0[t] = acc1[t] = 0.0f;
 #pragma unroll
         for (int j = 0; j < P::S; ++j) {
             const uint32_t * cpa = reinterpret_cast<const uint32_t *>(ub + cw_al + SLOT_BYTES * j);
             const uint32_t w0 = __builtin_amdgcn_alignbyte(cpa[1], cpa[0], sh);
             const uint32_t w1 = __builtin_amdgcn_alignbyte(cpa[2], cpa[1], sh);
             const uint32_t dwb = *reinterpret_cast<const uint16_t *>(ub + dwo + SLOT_BYTES * j);
-            const int s = chunk_dot_nib(w0, w1, ah[j], al[j], bias[j]);
             const bool second = (P::G == 2) && (j > P::SPLIT || (j == P::SPLIT && lane >= 32));
-            if (DUMP) {
-                const int v = 64 * j + lane;
-                const int row = u * P::G + (second ? 1 : 0);
-                if (v < P::G * P::NCH && row < mg.n_out[0])     // single matrix
-                    dump[(size_t)row * P::NCH + (second ? v - P::NCH : v)] = s;
-            } else {
-                const float t = da[j] * (float)s;
-                float dw = f16_bits_to_f32(dwb);
-                if (P::PARTIAL && j == P::S - 1) dw = lane < 32 ? dw : 0.0f;   // idle lanes: LDS past the unit
-                if (P::G == 1 || j < P::SPLIT) acc0 = fmaf(dw, t, acc0);
-                else if (j > P::SPLIT) acc1 = fmaf(dw, t, acc1);
-                else if (lane < 32) acc0 = fmaf(dw, t, acc0);
-                else acc1 = fmaf(dw, t, acc1);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const int s = chunk_dot_nib(w0, w1, ah[t][j], al[t][j], bias[t][j]);
+                if (DUMP) {
+                    const int v = 64 * j + lane;
+                    const int row = u * P::G + (second ? 1 : 0);
+                    if (v < P::G * P::NCH && row < mg.n_out[0])     // single matrix
+                        dump[(size_t)row * P::NCH + (second ? v - P::NCH : v)] = s;
+                } else {
+                    const float ts = da[t][j] * (float)s;
+                    float dw = f16_bits_to_f32(dwb);
+                    if (P::PARTIAL && j == P::S - 1) dw = lane < 32 ? dw : 0.0f;   // idle lanes: LDS past the unit
+                    if (P::G == 1 || j < P::SPLIT) acc0[t] = fmaf(dw, ts, acc0[t]);
+                    else if (j > P::SPLIT) acc1[t] = fmaf(dw, ts, acc1[t]);
+                    else if (lane < 32) acc0[t] = fmaf(dw, ts, acc0[t]);
+                    else acc1[t] = fmaf(dw, ts, acc1[t]);
+                }
             }
         }
         if (!DUMP) {
-            if (P::G == 2) {
-                const float v = wave_sum2_to_lanes31_63(acc0, acc1);
-                const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
-                const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-                ykeep = (lane == 2 * i) ? t0 : ((lane == 2 * i + 1) ? t1 : ykeep);
-            } else {
-                const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_to_lane63(acc0)), 63));
-                ykeep = (lane == i) ? t0 : ykeep;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                if (P::G == 2) {
+                    const float v = wave_sum2_to_lanes31_63(acc0[t], acc1[t]);
+                    const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+                    const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+                    ykeep = (lane == 2 * i * NT + t) ? t0 : ((lane == (2 * i + 1) * NT + t) ? t1 : ykeep);
+                } else {
+                    const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_to_lane63(acc0[t])), 63));
+                    ykeep = (lane == i * NT + t) ? t0 : ykeep;
+                }
             }
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);        // lgkmcnt(0): this slot's reads are done
         __builtin_amdgcn_wave_barrier();
     } while (++i < nu);
-    if (!DUMP && lane < nu * P::G) {
+    if (!DUMP && lane < nu * P::G * NT) {
         const uint8_t * Wm;
         float * ym;
         int n_out_m, lu;
-        gs.at(gw + (lane / P::G) * NW, Wm, ym, n_out_m, lu);
-        const int row = lu * P::G + lane % P::G;
-        if (row < n_out_m) ym[row] = ykeep;
+        const int rt = lane / NT, t = lane - NT * rt;        // (G i + r), token
+        gs.at(gw + (rt / P::G) * NW, Wm, ym, n_out_m, lu);
+        const int row = lu * P::G + rt % P::G;
+        if (NT == 1) {
+            if (row < n_out_m) ym[row] = ykeep;
+        } else if (row < n_out_m && t < n_tok) {
+            ym[(size_t)row * n_tok + t] = ykeep;
+        }
     }
 }
 
@@ -657,10 +694,10 @@ int default_wg_per_cu(int nb, int64_t w_bytes) {
 }
 
 // LDS bytes of one gemv_nb_kernel workgroup (all static allocations)
-template <int NB, int D, int WAVES, int ROT>
+template <int NB, int D, int WAVES, int ROT, int NT = 1>
 constexpr int nb_lds_bytes() {
-    using P = NbSpec<NB>;
-    constexpr int act = (Q81_BYTES * P::NCH + 1023) / 1024 * 1024;
+    using P = NbSpec<NB, NT>;
+    constexpr int act = (Q81_BYTES * P::NCH * NT + 1023) / 1024 * 1024;
     constexpr int ring = WAVES * (D + 1) * P::LDSB;
     constexpr int nhb = P::NCH / 32;
     constexpr int stage = (ROT ? nhb * HBLK * 4 : 0) + (ROT == 2 ? nhb * HBLK * 4 : 0);
@@ -682,11 +719,11 @@ bool group_units(MatGroup & mg, int n_mat) {
     return u < 0x40000000;
 }
 
-template <int NB, int D, int WAVES, bool DUMP, int ROT = 0>
+template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, int NT = 1>
 int launch_nb_t(MatGroup mg, int n_mat, const void * xin, const float * signs, int32_t * dump,
-                int per_cu, hipStream_t st) {
-    using P = NbSpec<NB>;
-    constexpr int lds = nb_lds_bytes<NB, D, WAVES, ROT>();
+                int per_cu, hipStream_t st, int n_tok = 1) {
+    using P = NbSpec<NB, NT>;
+    constexpr int lds = nb_lds_bytes<NB, D, WAVES, ROT, NT>();
     static_assert(lds <= LDS_PER_CU, "workgroup LDS");
     if (!group_units<P::G>(mg, n_mat)) return 1;
     const int n_units = mg.u0[MAX_GROUP];
@@ -698,16 +735,19 @@ int launch_nb_t(MatGroup mg, int n_mat, const void * xin, const float * signs, i
     if (blocks > max_blocks) blocks = max_blocks;
     const int NW = blocks * WAVES;
     int upw = (n_units + NW - 1) / NW;
-    if (upw > 64 / P::G) {                      // one output per lane of a wave
-        upw = 64 / P::G;
+    if (upw > 64 / (P::G * NT)) {               // one output per lane of a wave
+        upw = 64 / (P::G * NT);
         blocks = (n_units + upw * WAVES - 1) / (upw * WAVES);
     }
-    if (n_mat > 1)
+    if constexpr (NT > 1)
+        hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, 0, false, NT>), dim3(blocks), dim3(64 * WAVES),
+                           0, st, mg, xin, signs, dump, upw, n_tok);
+    else if (n_mat > 1)
         hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, DUMP, ROT, true>), dim3(blocks), dim3(64 * WAVES), 0,
-                           st, mg, xin, signs, dump, upw);
+                           st, mg, xin, signs, dump, upw, 1);
     else
         hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, DUMP, ROT, false>), dim3(blocks), dim3(64 * WAVES), 0,
-                           st, mg, xin, signs, dump, upw);
+                           st, mg, xin, signs, dump, upw, 1);
     return (int)hipGetLastError();
 }
 
@@ -724,6 +764,34 @@ int launch_nb(const MatGroup & mg, int n_mat, const uint8_t * xq, int32_t * dump
     int per_cu = env_int("BONSAI_GEMV_WG_PER_CU", 0);
     if (per_cu <= 0) per_cu = default_wg_per_cu(NB, group_weight_bytes(mg, n_mat, NB));
     return launch_nb_t<NB, 2, 4, DUMP>(mg, n_mat, xq, nullptr, dump, per_cu, st);
+}
+
+// Small batch on the streaming kernel: n_tok <= NT tokens (2 or 3), chunk-major Xq.
+// Instantiated where the per-token planes fit in registers: NT * S * 10
+// registers of activation per lane, at most 120 where three waves share a
+// SIMD, at most 400 for the widest rows (one workgroup, one wave per SIMD).
+template <int NB, int NT>
+constexpr bool nt_fits() { return NT * NbSpec<NB, NT>::S * 10 <= (NB >= 96 ? 400 : 120); }
+
+template <int NB, int NT>
+int launch_nb_small(const uint8_t * W, const uint8_t * X, float * Y, int n_out, int n_tok, hipStream_t st) {
+    if constexpr (!nt_fits<NB, NT>()) {
+        return -1;
+    } else {
+        MatGroup mg = single_group(W, Y, n_out);
+        int per_cu = env_int("BONSAI_GEMV_WG_PER_CU", 0);
+        if (per_cu <= 0) per_cu = default_wg_per_cu(NB, (int64_t)n_out * PQ2_BYTES * NB);
+        return launch_nb_t<NB, 2, 4, false, 0, NT>(mg, 1, X, nullptr, nullptr, per_cu, st, n_tok);
+    }
+}
+
+template <int NB>
+int launch_nb_small_nt(const uint8_t * W, const uint8_t * X, float * Y, int n_out, int n_tok, hipStream_t st) {
+    switch (n_tok) {
+        case 2: return launch_nb_small<NB, 2>(W, X, Y, n_out, n_tok, st);
+        case 3: return launch_nb_small<NB, 3>(W, X, Y, n_out, n_tok, st);
+        default: return -1;
+    }
 }
 
 // Fused rotation: every workgroup rotates the whole activation, so the
@@ -904,15 +972,35 @@ int make_group(MatGroup & mg, const void * const * W, float * const * y, const i
     return 0;
 }
 
-MatGroup single_group(const void * W, float * y, int64_t n_out) {
-    MatGroup mg{};
-    mg.W[0] = static_cast<const uint8_t *>(W);
-    mg.y[0] = y;
-    mg.n_out[0] = (int)n_out;
-    return mg;
+}  // namespace
+
+namespace pq2 {
+
+// Small batch (2..3 tokens) on the streaming GEMV kernel, for the GEMM's
+// dispatcher: returns -1 when the shape or alignment has no such kernel
+// (BONSAI_GEMM_SMALL_GEMV = 1 turns it off, 2 limits it to two tokens).  Measured on MI355X (us, against the MFMA small-batch kernel):
+// 17408x5120 B=2 10.0 / 12.8, B=3 12.4 / 13.1; 5120x17408 B=2 10.9 / 16.3,
+// B=3 16.1 / 16.9; at B=4 the MFMA kernel is faster (13.1 vs 15.7).
+int gemv_small_batch(const void * W, const void * Xq, float * Y, int64_t n_out, int64_t n_in,
+                     int64_t n_tok, bonsai_stream stream) {
+    if (n_tok < 2 || n_tok > 3 || n_out <= 0 || n_out > 0x3fffffff) return -1;
+    if (((uintptr_t)W & 15u) != 0 || ((uintptr_t)Xq & 15u) != 0) return -1;
+    if (n_tok > env_int("BONSAI_GEMM_SMALL_GEMV", 3)) return -1;
+    const uint8_t * w = static_cast<const uint8_t *>(W);
+    const uint8_t * x = static_cast<const uint8_t *>(Xq);
+    hipStream_t st = (hipStream_t)stream;
+    switch (n_in / QK_PQ2) {
+        case 8: return launch_nb_small_nt<8>(w, x, Y, (int)n_out, (int)n_tok, st);
+        case 40: return launch_nb_small_nt<40>(w, x, Y, (int)n_out, (int)n_tok, st);
+        case 48: return launch_nb_small_nt<48>(w, x, Y, (int)n_out, (int)n_tok, st);
+        case 80: return launch_nb_small_nt<80>(w, x, Y, (int)n_out, (int)n_tok, st);
+        case 96: return launch_nb_small_nt<96>(w, x, Y, (int)n_out, (int)n_tok, st);
+        case 136: return launch_nb_small_nt<136>(w, x, Y, (int)n_out, (int)n_tok, st);
+        default: return -1;
+    }
 }
 
-}  // namespace
+}  // namespace pq2
 
 extern "C" {
 
