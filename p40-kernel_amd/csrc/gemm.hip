@@ -655,13 +655,13 @@ int skinny_lds_limit() {
 }
 
 // ---------------------------------------------------------------------------
-// f16-MFMA prefill GEMM.  v_mfma_f32_16x16x32_f16 with A = (code - 1) and B = q
-// as f16: both are small integers, exact in f16, and the MFMA's fp32
-// accumulation of 32 products stays exact (|S| <= 8128 < 2^24), so each
-// MFMA returns the chunk dot S already as an fp32 value.  The per-chunk
-// activation scale then costs one FMA per output element (the int8 MFMA
-// needs a convert and an FMA), and the per-block weight scale one FMA per
-// element per 4 chunks.
+// f16-MFMA prefill GEMM.  v_mfma_f32_16x16x32_f16 with A = (code - 1) * dw
+// and B = q as f16: (code - 1) * dw is exact in f16 (code - 1 is -1, 0, 1 or
+// 2), q is a small integer, every product is exact in fp32 and every partial
+// sum is dw times an integer of at most 13 bits (|S| <= 8128), so each MFMA
+// returns dw * S exactly.  The per-chunk activation scale then costs one FMA
+// per output element (the int8 MFMA needs a convert and an FMA), and the
+// weight scale nothing beyond one packed f16 multiply per two staged codes.
 //
 // Workgroup: 512 threads (8 waves as 2 x 4), tile 128 rows x 128 tokens; a
 // wave owns 64 rows x 32 tokens = 4 x 2 MFMA tiles of 16 x 16.  Per PQ2_0
@@ -698,6 +698,11 @@ __device__ __forceinline__ uint32_t sub1152_f16x2(uint32_t x) {
     return __builtin_bit_cast(uint32_t, r);
 }
 
+__device__ __forceinline__ uint32_t mul_f16x2(uint32_t a, uint32_t b) {
+    const v2h r = __builtin_bit_cast(v2h, a) * __builtin_bit_cast(v2h, b);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
 __device__ __forceinline__ void q4_to_f16(uint32_t q4, uint32_t & lo, uint32_t & hi) {
     const uint32_t x = q4 ^ 0x80808080u;                               // q + 128 per byte
     lo = sub1152_f16x2(__builtin_amdgcn_perm(x, 0x64646464u, 0x00050004u));
@@ -716,7 +721,6 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
     __shared__ __attribute__((aligned(16))) uint8_t sA[2][GF_STAGE_A];
     __shared__ __attribute__((aligned(16))) uint8_t sB[2][GF_STAGE_B];
     __shared__ __attribute__((aligned(16))) float sDa[2][4][GF_BN];
-    __shared__ __attribute__((aligned(16))) float sDw[2][GF_BM];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -760,7 +764,7 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
         const bool tail = aa + 12 > w_bytes;
         r.a2 = *reinterpret_cast<const uint32_t *>(W + (tail ? aa + 6 : aa + 8));
         r.sh |= (tail ? 4u : 0u) | (pf_block < nb ? 8u : 0u);
-        r.dw = (uint32_t)*reinterpret_cast<const uint16_t *>(W + a_off - 2);
+        r.dw = (uint32_t)*reinterpret_cast<const uint16_t *>(W + a_off - 2 - 8 * ap);   // block scale
         const uint32_t * xb = reinterpret_cast<const uint32_t *>(b_ptr);
 #pragma unroll
         for (int k = 0; k < 9; ++k) r.q[k] = xb[k];
@@ -773,6 +777,7 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
     // (part q writes 16-byte group q of every A and B row) so that it can be
     // interleaved with the four chunk steps of the current block.
     uint32_t cw0, cw1;                                         // realigned code words
+    uint32_t dw2;                                              // the row's block scale, f16 x 2
     auto commit_part = [&](const Raw & r, int st, int q) {
         if (q == 0) {
             const uint32_t sh = r.sh & 3u;
@@ -784,7 +789,10 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
             // a block past the end (the padding step of an odd block count) gets
             // zero scales, so its products add exactly nothing
             const bool live = (r.sh & 8u) != 0;
-            if (ap == 0) sDw[st][ar] = (a_ok && live) ? f16_bits_to_f32(r.dw) : 0.0f;
+            // the weight scale rides in A: (code - 1) * dw is exact in f16
+            // (code - 1 is -1, 0, 1 or 2); a dead row or block gets scale 0
+            const uint32_t dwh = (a_ok && live) ? (r.dw & 0xffffu) : 0u;
+            dw2 = dwh | (dwh << 16);
             sDa[st][bp][bt] = (b_ok && live) ? f16_bits_to_f32(r.q[0] & 0xffffu) : 0.0f;
         }
         const uint32_t w = q < 2 ? cw0 : cw1;
@@ -792,6 +800,7 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
         uint32_t o0, o1, o2, o3;
         codes4_to_f16((w >> (2 * k0)) & 0x03030303u, o0, o1);
         codes4_to_f16((w >> (2 * k0 + 2)) & 0x03030303u, o2, o3);
+        o0 = mul_f16x2(o0, dw2); o1 = mul_f16x2(o1, dw2); o2 = mul_f16x2(o2, dw2); o3 = mul_f16x2(o3, dw2);
         *reinterpret_cast<v4u *>(&sA[st][ap * GF_BM * 64] + gf_swz(ar, q)) = (v4u){o0, o1, o2, o3};
         q4_to_f16(b_ok ? r.q[1 + 2 * q] : 0u, o0, o1);
         q4_to_f16(b_ok ? r.q[2 + 2 * q] : 0u, o2, o3);
@@ -826,7 +835,6 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
         // chunk pipeline: the MFMAs of chunk p+1 are issued before the epilogue
         // of chunk p, and a quarter of the next block's conversion follows each
         // epilogue, so VALU work runs while the matrix core is busy
-        float inner[4][2][4];
         v4f S[2][4][2];
         float da[2][2];
         auto issue = [&](int p) {
@@ -855,8 +863,7 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
                 for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        inner[mi][ni][i] = p == 0 ? da[0][ni] * S[0][mi][ni][i]
-                                                  : fmaf(da[p & 1][ni], S[p & 1][mi][ni][i], inner[mi][ni][i]);
+                        acc[mi][ni][i] = fmaf(da[p & 1][ni], S[p & 1][mi][ni][i], acc[mi][ni][i]);
             // pin the chunk's epilogue here: without it the compiler sinks all
             // the FMAs below the last MFMA and keeps every result live
 #pragma unroll
@@ -864,7 +871,7 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
 #pragma unroll
                 for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(inner[mi][ni][i]));
+                    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[mi][ni][i]));
         };
         issue(0);
 #pragma unroll
@@ -875,15 +882,6 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
             __builtin_amdgcn_sched_barrier(0);
             commit_part(next, st ^ 1, p);
             __builtin_amdgcn_sched_barrier(0);
-        }
-        // per-row block scale: output rows 4g + i of each 16-row tile
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi) {
-            const v4f dw = *reinterpret_cast<const v4f *>(&sDw[st][wm * 64 + 16 * mi + 4 * g]);
-#pragma unroll
-            for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[mi][ni][i] = fmaf(dw[i], inner[mi][ni][i], acc[mi][ni][i]);
         }
         __syncthreads();
     };

@@ -416,6 +416,25 @@ def test_gemm_small_batch_streaming(n_out, n_in, n_tok):
             assert normwise(got[:, t], host(y)) <= 2 * TOL
 
 
+def test_gemm_subnormal_and_zero_block_scales():
+    """Blocks whose fp16 scale is subnormal or zero (the prefill kernel
+    multiplies the scale into its f16 operand)."""
+    case("gemm 200x2048x64 with subnormal / zero block scales")
+    n_out, n_in, n_tok = 200, 2048, 64
+    W = O.gen_weights(1500, n_out, n_in).copy()
+    nb = n_in // 128
+    rng = np.random.default_rng(3)
+    for r in range(n_out):
+        for b in rng.choice(nb, 3, replace=False):
+            off = (r * nb + b) * 34
+            W[off:off + 2] = np.frombuffer(np.uint16(rng.integers(0, 1024)).tobytes(), np.uint8)
+    X = O.gen_normal(1501, n_tok * n_in).reshape(n_tok, n_in)
+    Xq = O.quantize_chunk_major(X)
+    Y = torch.full((n_out, n_tok), float("nan"), dtype=torch.float32, device="cuda")
+    B.gemm(dev(W), dev(Xq), Y, n_out, n_in, n_tok)
+    assert normwise(host(Y), O.gemm(W, Xq, n_out, n_in, n_tok, nthreads=16)) <= TOL
+
+
 def test_gemm_equals_gemv_per_token():
     case("gemm n_tok=3 equals three gemv")
     n_out, n_in, n_tok = 300, 5120, 3
