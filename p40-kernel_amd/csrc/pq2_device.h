@@ -147,19 +147,30 @@ __device__ __forceinline__ void nib_planes(const uint32_t (&a)[8], uint32_t (&h)
     }
 }
 
+// The four nibble words of a chunk's two code words.
+__device__ __forceinline__ void code_nibbles(uint32_t w0, uint32_t w1, uint32_t (&n)[4]) {
+    constexpr uint32_t M = 0x33333333u;
+    n[0] = w0 & M; n[1] = (w0 >> 2) & M; n[2] = w1 & M; n[3] = (w1 >> 2) & M;
+}
+
+__device__ __forceinline__ int chunk_dot_nibw(const uint32_t (&n)[4], const uint32_t (&h)[4],
+                                              const uint32_t (&l)[4], int bias) {
+    int sh = __builtin_amdgcn_sdot8((int)n[0], (int)h[0], 0, false);
+    sh = __builtin_amdgcn_sdot8((int)n[1], (int)h[1], sh, false);
+    sh = __builtin_amdgcn_sdot8((int)n[2], (int)h[2], sh, false);
+    sh = __builtin_amdgcn_sdot8((int)n[3], (int)h[3], sh, false);
+    uint32_t sl = __builtin_amdgcn_udot8(n[0], l[0], (uint32_t)bias, false);
+    sl = __builtin_amdgcn_udot8(n[1], l[1], sl, false);
+    sl = __builtin_amdgcn_udot8(n[2], l[2], sl, false);
+    sl = __builtin_amdgcn_udot8(n[3], l[3], sl, false);
+    return (int)(((uint32_t)sh << 4) + sl);   // modulo 2^32: exact for |sumi| < 2^31
+}
+
 __device__ __forceinline__ int chunk_dot_nib(uint32_t w0, uint32_t w1, const uint32_t (&h)[4],
                                              const uint32_t (&l)[4], int bias) {
-    constexpr uint32_t M = 0x33333333u;
-    const uint32_t n0 = w0 & M, n1 = (w0 >> 2) & M, n2 = w1 & M, n3 = (w1 >> 2) & M;
-    int sh = __builtin_amdgcn_sdot8((int)n0, (int)h[0], 0, false);
-    sh = __builtin_amdgcn_sdot8((int)n1, (int)h[1], sh, false);
-    sh = __builtin_amdgcn_sdot8((int)n2, (int)h[2], sh, false);
-    sh = __builtin_amdgcn_sdot8((int)n3, (int)h[3], sh, false);
-    uint32_t sl = __builtin_amdgcn_udot8(n0, l[0], (uint32_t)bias, false);
-    sl = __builtin_amdgcn_udot8(n1, l[1], sl, false);
-    sl = __builtin_amdgcn_udot8(n2, l[2], sl, false);
-    sl = __builtin_amdgcn_udot8(n3, l[3], sl, false);
-    return (int)(((uint32_t)sh << 4) + sl);   // modulo 2^32: exact for |sumi| < 2^31
+    uint32_t n[4];
+    code_nibbles(w0, w1, n);
+    return chunk_dot_nibw(n, h, l, bias);
 }
 
 __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
