@@ -52,9 +52,9 @@ int bonsai_p40_quant_activations(const float * x, void * out, int64_t n, bonsai_
 // Y[n_out, n_tok] (row-major, Y[r*n_tok + t]) = W . X, X in permuted Q8_1,
 // chunk-major: block (c, t) at index c*n_tok + t (src/kernels/gemm_p40.cu:75).
 // Replaces include/bonsai_p40.h:29-30 (src/kernels/gemm_p40.cu:143-154).
-// n_tok == 1 runs the decode GEMV, 2..3 tokens the streaming GEMV kernel
-// with per-token activation planes, 4..16 the small-batch MFMA kernel, larger
-// n_tok the f16-MFMA tile GEMM.  Errors: 1 if n_in <= 0 or n_in % 128 != 0;
+// n_tok == 1 runs the decode GEMV, 2..4 tokens streaming kernels (per-token
+// activation planes, or 4x4x4 int8 MFMA), 5..16 the small-batch MFMA
+// kernel, larger n_tok the f16-MFMA tile GEMM.  Errors: 1 if n_in <= 0 or n_in % 128 != 0;
 // 0 (no-op) if n_out <= 0 or n_tok <= 0.
 int bonsai_p40_gemm(const void * W, const void * Xq, float * Y,
                     int64_t n_out, int64_t n_in, int64_t n_tok, bonsai_stream stream);

@@ -907,7 +907,7 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
 }  // namespace
 
 namespace pq2 {
-// gemv.hip: 2..4 tokens on the streaming GEMV kernel; -1 if not applicable
+// gemv.hip: 2..4 tokens on the streaming kernels; -1 if not applicable
 int gemv_small_batch(const void * W, const void * Xq, float * Y, int64_t n_out, int64_t n_in,
                      int64_t n_tok, bonsai_stream stream);
 }

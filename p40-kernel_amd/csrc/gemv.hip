@@ -766,6 +766,217 @@ int launch_nb(const MatGroup & mg, int n_mat, const uint8_t * xq, int32_t * dump
     return launch_nb_t<NB, 2, 4, DUMP>(mg, n_mat, xq, nullptr, dump, per_cu, st);
 }
 
+// ---------------------------------------------------------------------------
+// Small batch, 4..8 tokens: v_mfma_i32_4x4x4i8 on the streaming scheme.
+// The instruction computes 16 independent 4x4 blocks; block b of lane group
+// 4b..4b+3 takes A row i from lane 4b+i and B column j from lane 4b+j (4
+// int8 along K in one dword each) and returns D(row i, column j) in register
+// i of lane 4b+j.  Here a unit is 4 consecutive weight rows, a slot 16 chunks
+// of it: block b = chunk 16s+b, its 4 rows = the unit's rows, its 4 columns =
+// 4 tokens.  Eight instructions (K = 4 each) cover a chunk: instruction q
+// takes the code bytes (w_{q/4} >> 2(q%4)) & 0x03030303 -- exactly the
+// positions of permuted activation word q -- and the accumulator starts at
+// -s, so D is the integer chunk dot sum (code-1) q with no idle columns.  The
+// 16 chunk partial sums of a (row, token) meet at the end of the unit (row
+// rotations, then permlane swaps).  The chunk-major X of all tokens sits in
+// LDS; units stream through a 2-slot LDS ring by DMA.  NTG groups of 4
+// tokens share the code words; the dispatcher uses one group (3..4 tokens):
+// two groups measured no faster than the 16x16 MFMA kernel.
+template <int NB>
+struct Mfma4Spec {
+    static constexpr int NCH = 4 * NB;
+    static constexpr int NS = NCH / 16;                  // slots per unit
+    static constexpr int RB = PQ2_BYTES * NB;            // bytes per row
+    static constexpr int UB = 4 * RB;                    // bytes per unit
+    static constexpr int NPIECE = UB / 16;
+    static constexpr int NPL = (NPIECE + 63) / 64;
+    static constexpr int LDSB = (UB + 16 > 1024 * NPL) ? UB + 16 : 1024 * NPL;
+    static_assert(NCH % 16 == 0 && UB % 16 == 0 && RB % 4 == 0, "unit shape");
+};
+
+template <int NB, int NTG, int WAVES>
+constexpr int mfma4_lds_bytes() {
+    using P = Mfma4Spec<NB>;
+    return (Q81_BYTES * P::NCH * 4 * NTG + 1023) / 1024 * 1024 + WAVES * 2 * P::LDSB;
+}
+
+constexpr int DPP_ROW_ROR4 = 0x124, DPP_ROW_ROR8 = 0x128;
+
+template <int NB, int NTG, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES)
+gemv_mfma4_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X, float * __restrict__ Y,
+                  int n_out, int n_tok, int units_per_wave) {
+    using P = Mfma4Spec<NB>;
+    typedef int v4i_t __attribute__((ext_vector_type(4)));
+    constexpr int ACT_MAX = Q81_BYTES * P::NCH * 4 * NTG;
+    __shared__ __attribute__((aligned(16))) uint8_t act_lds[(ACT_MAX + 1023) / 1024 * 1024];
+    __shared__ __attribute__((aligned(16))) uint8_t ring_all[WAVES][2][P::LDSB];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    __builtin_assume(lane >= 0 && lane < 64);
+    uint8_t (*ring)[P::LDSB] = ring_all[wave];
+    const int n_units = (n_out + 3) / 4;
+    const int n_full = n_out / 4;
+    const int gw = wave * gridDim.x + blockIdx.x;
+    const int NW = gridDim.x * WAVES;
+    const int nu = gw < n_units ? min(units_per_wave, (n_units - 1 - gw) / NW + 1) : 0;
+
+    // 1. this wave's share of the activation DMA
+    const int act_bytes = Q81_BYTES * P::NCH * n_tok;
+    const int na = (act_bytes + 1023) / 1024;
+    for (int k = wave; k < na; k += WAVES) {
+        const int off = min(16 * (64 * k + lane), act_bytes - 16);
+        __builtin_amdgcn_global_load_lds(X + off, (lds_void *)(&act_lds[1024 * k]), 16, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. unit DMA (a trailing unit with fewer than 4 rows clamps to the end of W)
+    uint32_t poff[P::NPL];
+#pragma unroll
+    for (int k = 0; k < P::NPL; ++k) poff[k] = 16u * (uint32_t)min(lane + 64 * k, P::NPIECE - 1);
+    const size_t last_piece = (size_t)n_out * P::RB / 16 - 1;
+    auto issue = [&](int uu, int slot) {
+        const uint8_t * base = W + (size_t)uu * P::UB;
+        const bool full = uu < n_full;
+#pragma unroll
+        for (int k = 0; k < P::NPL; ++k) {
+            const uint8_t * src = base + poff[k];
+            if (!full) {
+                size_t pc = (size_t)uu * (P::UB / 16) + poff[k] / 16;
+                src = W + 16 * (pc < last_piece ? pc : last_piece);
+            }
+            __builtin_amdgcn_global_load_lds(src, (lds_void *)(&ring[slot][1024 * k]), 16, 0, CPOL_NT);
+        }
+    };
+    __builtin_amdgcn_s_barrier();
+    if (nu > 0) issue(gw, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (nu > 0) wait_vmcnt<P::NPL>();
+    else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    if (nu <= 0) return;
+
+    // per-lane roles: row i of the unit, chunk offset b in the slot, token j of a group
+    const int i4 = lane & 3, b16 = lane >> 2;
+    const int cbase = i4 * P::RB + PQ2_BYTES * (b16 >> 2) + 2 + 8 * (b16 & 3);   // code bytes, slot 0
+    const int csh = cbase & 3;
+    const int c_al = cbase - csh;
+    const int dbase = i4 * P::RB + PQ2_BYTES * (b16 >> 2);                      // block scale, slot 0
+
+    // outputs stay in lanes until the end (a global store inside the unit
+    // loop makes the compiler wait for the next unit's DMA before the ring
+    // reads): lane 16 it + 4 r + j keeps (row r, token j) of unit it
+    float ykeep[NTG];
+#pragma unroll
+    for (int g = 0; g < NTG; ++g) ykeep[g] = 0.0f;
+    for (int it = 0; it < nu; ++it) {
+        const int slot = it & 1;
+        wait_vmcnt<0>();
+        __builtin_amdgcn_wave_barrier();
+        if (it + 1 < nu) issue(gw + (it + 1) * NW, slot ^ 1);   // the other slot's reads are done
+        const uint8_t * ub = ring[slot];
+        float acc[NTG][4];
+#pragma unroll
+        for (int g = 0; g < NTG; ++g)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[g][r] = 0.0f;
+#pragma unroll
+        for (int sl = 0; sl < P::NS; ++sl) {
+            const uint32_t * cpa = reinterpret_cast<const uint32_t *>(ub + c_al + 136 * sl);
+            const uint32_t w0 = __builtin_amdgcn_alignbyte(cpa[1], cpa[0], csh);
+            const uint32_t w1 = __builtin_amdgcn_alignbyte(cpa[2], cpa[1], csh);
+            // block scales of the 4 rows: each lane reads its own row's, the quad shares them
+            const float dwi = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(ub + dbase + 136 * sl));
+            float dwr[4];
+            dwr[0] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(dwi), 0x00, 0xf, 0xf, true));
+            dwr[1] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(dwi), 0x55, 0xf, 0xf, true));
+            dwr[2] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(dwi), 0xAA, 0xf, 0xf, true));
+            dwr[3] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(dwi), 0xFF, 0xf, 0xf, true));
+            const int c = 16 * sl + b16;
+#pragma unroll
+            for (int g = 0; g < NTG; ++g) {
+                const int t = 4 * g + i4;                      // this lane's token (column)
+                const bool tv = t < n_tok;
+                // unconditional reads (a missing token reads block 0 and is zeroed)
+                const uint32_t * ab = reinterpret_cast<const uint32_t *>(&act_lds[Q81_BYTES * (tv ? c * n_tok + t : 0)]);
+                uint32_t aw[9];
+#pragma unroll
+                for (int k = 0; k < 9; ++k) aw[k] = ab[k];
+                const uint32_t ds = tv ? aw[0] : 0u;
+                const int ns = -(int)(int16_t)(ds >> 16);
+                v4i_t d = {ns, ns, ns, ns};
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const uint32_t wq = q < 4 ? w0 : w1;
+                    const int a = (int)((wq >> (2 * (q & 3))) & 0x03030303u);
+                    const int bq = tv ? (int)aw[1 + q] : 0;
+                    d = __builtin_amdgcn_mfma_i32_4x4x4i8(a, bq, d, 0, 0, 0);
+                }
+                const float da = f16_bits_to_f32(ds & 0xffffu);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[g][r] = fmaf(dwr[r] * da, (float)d[r], acc[g][r]);
+            }
+        }
+        // sum the 16 chunk blocks of every (row, token): within a 16-lane row
+        // by rotations of 4 and 8 (they keep lane % 4, the token), then across
+        // the four rows by permlane16 and permlane32 swaps
+#pragma unroll
+        for (int g = 0; g < NTG; ++g) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = acc[g][r];
+                v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), DPP_ROW_ROR8, 0xf, 0xf, true));
+                v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), DPP_ROW_ROR4, 0xf, 0xf, true));
+                const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+                v = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+                const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+                v = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
+                ykeep[g] = (b16 == 4 * it + r) ? v : ykeep[g];  // every lane holds its token j's total
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);        // lgkmcnt(0): this slot's reads are done
+        __builtin_amdgcn_wave_barrier();
+    }
+    if (lane < 16 * nu) {
+        const int row = 4 * (gw + (lane >> 4) * NW) + ((lane >> 2) & 3);
+#pragma unroll
+        for (int g = 0; g < NTG; ++g) {
+            const int t = 4 * g + i4;
+            if (row < n_out && t < n_tok) Y[(size_t)row * n_tok + t] = ykeep[g];
+        }
+    }
+}
+
+template <int NB, int NTG, int WAVES>
+int launch_mfma4(const uint8_t * W, const uint8_t * X, float * Y, int n_out, int n_tok, hipStream_t st) {
+    constexpr int lds = mfma4_lds_bytes<NB, NTG, WAVES>();
+    static_assert(lds <= LDS_PER_CU, "workgroup LDS");
+    const int n_units = (n_out + 3) / 4;
+    int per_cu = env_int("BONSAI_MFMA4_WG_PER_CU", LDS_PER_CU / lds);
+    if (per_cu > LDS_PER_CU / lds) per_cu = LDS_PER_CU / lds;
+    if (per_cu < 1) per_cu = 1;
+    int blocks = per_cu * cu_count();
+    const int max_blocks = (n_units + WAVES - 1) / WAVES;
+    if (blocks > max_blocks) blocks = max_blocks;
+    int upw = (n_units + blocks * WAVES - 1) / (blocks * WAVES);
+    if (upw > 4) {                                  // 16 outputs per unit in the lanes of a wave
+        upw = 4;
+        blocks = (n_units + 4 * WAVES - 1) / (4 * WAVES);
+    }
+    hipLaunchKernelGGL((gemv_mfma4_kernel<NB, NTG, WAVES>), dim3(blocks), dim3(64 * WAVES), 0, st, W, X, Y,
+                       n_out, n_tok, upw);
+    return (int)hipGetLastError();
+}
+
+// 3..4 tokens: 8-wave workgroups for the large matrices, 4-wave ones (more
+// workgroups) below 4096 rows -- measured on MI355X.
+template <int NB>
+int launch_mfma4_nt(const uint8_t * W, const uint8_t * X, float * Y, int n_out, int n_tok, hipStream_t st) {
+    const int waves = env_int("BONSAI_MFMA4_WAVES", n_out >= 4096 ? 8 : 4);
+    if (waves == 4) return launch_mfma4<NB, 1, 4>(W, X, Y, n_out, n_tok, st);
+    return launch_mfma4<NB, 1, 8>(W, X, Y, n_out, n_tok, st);
+}
+
 // Small batch on the streaming kernel: n_tok <= NT tokens (2 or 3), chunk-major Xq.
 // Instantiated where the per-token planes fit in registers: NT * S * 10
 // registers of activation per lane, at most 120 where three waves share a
@@ -976,19 +1187,35 @@ int make_group(MatGroup & mg, const void * const * W, float * const * y, const i
 
 namespace pq2 {
 
-// Small batch (2..3 tokens) on the streaming GEMV kernel, for the GEMM's
-// dispatcher: returns -1 when the shape or alignment has no such kernel
-// (BONSAI_GEMM_SMALL_GEMV = 1 turns it off, 2 limits it to two tokens).  Measured on MI355X (us, against the MFMA small-batch kernel):
-// 17408x5120 B=2 10.0 / 12.8, B=3 12.4 / 13.1; 5120x17408 B=2 10.9 / 16.3,
-// B=3 16.1 / 16.9; at B=4 the MFMA kernel is faster (13.1 vs 15.7).
+// Small batch (2..4 tokens) on the streaming kernels, for the GEMM's
+// dispatcher; -1 when the shape or alignment has neither (the caller then
+// uses the MFMA small-batch kernel).  Measured on MI355X (us; per-token
+// planes / 4x4x4 MFMA / the MFMA small-batch kernel of gemm.hip):
+//   17408x5120  B=2 10.3 / 10.6 / 12.8   B=3 12.2 / 10.6 / 13.1   B=4 -- / 10.4 / 13.3
+//   6144x5120   B=2  6.6 /  6.1 /  7.2   B=3  6.7 /  6.2 /  7.4   B=4 -- /  6.2 /  7.5
+//   5120x6144   B=2  5.7 /  6.4 /  8.1   B=3  6.8 /  6.6 /  8.3   B=4 -- /  6.5 /  8.4
+//   5120x17408  B=2 10.9 /  -- / 16.3   B=3 16.1 /  -- / 16.9
+// so 2 tokens take the planes kernel, 3..4 the 4x4x4 kernel on its widths
+// (8, 40, 48 blocks per row), 3 tokens the planes kernel elsewhere.
+// BONSAI_GEMM_SMALL_GEMV = 1 turns both off.
+
 int gemv_small_batch(const void * W, const void * Xq, float * Y, int64_t n_out, int64_t n_in,
                      int64_t n_tok, bonsai_stream stream) {
-    if (n_tok < 2 || n_tok > 3 || n_out <= 0 || n_out > 0x3fffffff) return -1;
+    if (n_tok < 2 || n_tok > 4 || n_out <= 0 || n_out > 0x3fffffff) return -1;
     if (((uintptr_t)W & 15u) != 0 || ((uintptr_t)Xq & 15u) != 0) return -1;
-    if (n_tok > env_int("BONSAI_GEMM_SMALL_GEMV", 3)) return -1;
+    if (n_tok > env_int("BONSAI_GEMM_SMALL_GEMV", 4)) return -1;
     const uint8_t * w = static_cast<const uint8_t *>(W);
     const uint8_t * x = static_cast<const uint8_t *>(Xq);
     hipStream_t st = (hipStream_t)stream;
+    const int nb = (int)(n_in / QK_PQ2);
+    if (n_tok >= env_int("BONSAI_MFMA4_MIN_TOK", 3) && (nb == 8 || nb == 40 || nb == 48)) {
+        switch (nb) {
+            case 8: return launch_mfma4_nt<8>(w, x, Y, (int)n_out, (int)n_tok, st);
+            case 40: return launch_mfma4_nt<40>(w, x, Y, (int)n_out, (int)n_tok, st);
+            default: return launch_mfma4_nt<48>(w, x, Y, (int)n_out, (int)n_tok, st);
+        }
+    }
+    if (n_tok > 3) return -1;
     switch (n_in / QK_PQ2) {
         case 8: return launch_nb_small_nt<8>(w, x, Y, (int)n_out, (int)n_tok, st);
         case 40: return launch_nb_small_nt<40>(w, x, Y, (int)n_out, (int)n_tok, st);

@@ -392,10 +392,10 @@ def test_gemm_prefill_shapes_row_sample(n_out, n_in, n_tok):
     (333, 1024, 3), (64, 10240, 2), (31, 12288, 2), (17407, 5120, 2), (5120, 17408, 2),
     (301, 17408, 3), (100, 17408, 4), (257, 12288, 4)])
 def test_gemm_small_batch_streaming(n_out, n_in, n_tok):
-    """2..3 tokens run on the streaming GEMV kernel (per-token planes), 4 on
-    the MFMA small-batch kernel: against the oracle, and against one GEMV per
-    token (bit-identical where the streaming kernel's unit shape is the
-    GEMV's: 2 tokens, or widths with one-row units)."""
+    """2 tokens run on the streaming GEMV kernel with per-token planes (3 on
+    the widths without a 4x4x4 kernel), 3..4 on the 4x4x4 MFMA kernel:
+    against the oracle, and against one GEMV per token (bit-identical for 2
+    tokens, where the unit shape and the arithmetic are the GEMV's)."""
     case(f"gemm small batch {n_out}x{n_in}x{n_tok}")
     W = O.gen_weights(1400 + n_out + n_tok, n_out, n_in)
     X = np.stack([O.fwht(O.gen_normal(1401 + t + n_in, n_in)) for t in range(n_tok)])
@@ -406,7 +406,7 @@ def test_gemm_small_batch_streaming(n_out, n_in, n_tok):
     got = host(Y)
     assert np.all(np.isfinite(got))
     assert normwise(got, O.gemm(W, Xq, n_out, n_in, n_tok, nthreads=16)) <= TOL
-    same_units = n_tok == 2 or (n_tok == 3 and (4 * (n_in // 128)) % 64 == 0)
+    same_units = n_tok == 2
     for t in range(n_tok):
         y = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
         B.gemv(Wd, dev(O.quantize_q8_1(X[t], True)), y, n_out, n_in)
@@ -414,6 +414,29 @@ def test_gemm_small_batch_streaming(n_out, n_in, n_tok):
             np.testing.assert_array_equal(bits(got[:, t]), bits(host(y)))
         else:
             assert normwise(got[:, t], host(y)) <= 2 * TOL
+
+
+@pytest.mark.parametrize("n_out,n_in,n_tok", [
+    (17408, 5120, 4), (17408, 5120, 3), (6144, 5120, 4), (5121, 6144, 3), (33, 1024, 4),
+    (17407, 5120, 4), (1026, 6144, 4), (7, 5120, 3), (4095, 5120, 4), (4096, 5120, 3)])
+def test_gemm_small_batch_mfma4(n_out, n_in, n_tok):
+    """3..4 tokens on the 4x4x4 MFMA streaming kernel (4- and 8-wave
+    workgroups either side of 4096 rows): against the oracle and against one
+    GEMV per token."""
+    case(f"gemm small batch (mfma4) {n_out}x{n_in}x{n_tok}")
+    W = O.gen_weights(1600 + n_out + n_tok, n_out, n_in)
+    X = np.stack([O.fwht(O.gen_normal(1601 + t + n_in, n_in)) for t in range(n_tok)])
+    Xq = O.quantize_chunk_major(X)
+    Wd = dev(W)
+    Y = torch.full((n_out, n_tok), float("nan"), dtype=torch.float32, device="cuda")
+    B.gemm(Wd, dev(Xq), Y, n_out, n_in, n_tok)
+    got = host(Y)
+    assert np.all(np.isfinite(got))
+    assert normwise(got, O.gemm(W, Xq, n_out, n_in, n_tok, nthreads=16)) <= TOL
+    for t in range(n_tok):
+        y = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+        B.gemv(Wd, dev(O.quantize_q8_1(X[t], True)), y, n_out, n_in)
+        assert normwise(got[:, t], host(y)) <= 2 * TOL
 
 
 def test_gemm_subnormal_and_zero_block_scales():
