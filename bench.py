@@ -303,6 +303,8 @@ def main():
                     help="small-batch GEMM 17408x5120 with B tokens only (profiling)")
     ap.add_argument("--only-fused", action="store_true",
                     help="fused FWHT+Q8_1+GEMV 17408x5120 from fp32 only (profiling)")
+    ap.add_argument("--only-sweep", default="", metavar="MODE", choices=["", "separate", "fused", "grouped"],
+                    help="config-2 token sweep in one mode only (profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -335,6 +337,12 @@ def main():
         else:
             gbs = gemv_bytes(N_FF, N_EMBD, m) / (ms * 1e-3) / 1e9
             print(f"[bench] small batch 17408x5120 B={m}: {ms * 1e3:.2f} us  {gbs:.1f} GB/s", file=sys.stderr, flush=True)
+        return
+
+    if args.only_sweep:
+        ms, wb = bench_token_sweep(max(1, args.steps), min(args.warmup, 2), gen, mode=args.only_sweep)
+        print(f"[bench] token sweep {args.only_sweep}: {ms:.3f} ms/token  {wb / (ms * 1e-3) / 1e9:.1f} GB/s",
+              file=sys.stderr, flush=True)
         return
 
     if args.only_fused:
