@@ -165,6 +165,22 @@ def bench_fwht_gemv(n_out, n_in, steps, warmup, gen):
     return ms
 
 
+def bench_gemv_repack(n_out, n_in, steps, warmup, gen):
+    """bonsai_p40_gemv_repack (fp32 activation, quantised inside) on weights
+    repacked once with bonsai_p40_repack, over rotating copies."""
+    W0 = synth_weights(n_out, n_in, gen)
+    Wr = torch.empty_like(W0)
+    B.repack(W0, Wr, n_out, n_in)
+    R = copies_for(Wr.numel())
+    Ws = [Wr] + [Wr.clone() for _ in range(R - 1)]
+    del W0
+    x = torch.randn(n_in, generator=gen, device="cuda")
+    y = torch.empty(n_out, dtype=torch.float32, device="cuda")
+    ms = time_loop(lambda i: B.gemv_repack(Ws[i % R], x, y, n_out, n_in), steps, warmup)
+    del Ws
+    return ms
+
+
 def bench_prepass(n, steps, warmup, gen):
     x = torch.randn(n, generator=gen, device="cuda")
     q = torch.empty(B.q8_bytes(n), dtype=torch.uint8, device="cuda")
@@ -383,6 +399,13 @@ def main():
         for n in (N_EMBD, N_FF):
             m = bench_prepass(n, args.steps, args.warmup, gen)
             extra[f"fwht_quant_{n}_us"] = round(m * 1e3, 3)
+        for (n_out, n_in) in ((N_FF, N_EMBD), (N_EMBD, N_FF)):
+            m = bench_gemv_repack(n_out, n_in, args.steps, args.warmup, gen)
+            extra[f"gemv_repack_{n_out}x{n_in}"] = {
+                "us": round(m * 1e3, 3), "weight_GB/s": round(gemv_bytes(n_out, n_in) / (m * 1e-3) / 1e9, 1),
+                "note": "repacked weights, fp32 activation quantised inside (bonsai_p40_gemv_repack)"}
+            print(f"[bench] gemv_repack {n_out}x{n_in}: {extra[f'gemv_repack_{n_out}x{n_in}']}",
+                  file=sys.stderr, flush=True)
         for (n_out, n_in) in ((N_FF, N_EMBD), (N_EMBD, N_FF)):
             m = bench_fwht_gemv(n_out, n_in, args.steps, args.warmup, gen)
             extra[f"fwht_gemv_{n_out}x{n_in}"] = {

@@ -334,12 +334,19 @@ __device__ __forceinline__ float * rot_sign_stage() {
 // keeps the nibble planes of its chunk for each token, so a unit's code words
 // are extracted once and dotted against NT activations.  Tokens past n_tok
 // have zero planes; y is [n_out][n_tok].
-template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, bool GROUP = false, int NT = 1>
+//
+// ROT = 3 quantises the fp32 activation without the rotation.  RP: the
+// weights are in the aligned repacked layout (a row's fp16 scales first, then
+// unit p*nb + b = the 8 code bytes of chunk p of block b): the DMA moves the
+// same rows, only the lane's LDS offsets change (8-byte aligned code words,
+// no realignment).
+template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, bool GROUP = false, int NT = 1, bool RP = false>
 __global__ void __launch_bounds__(64 * WAVES)
 gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * __restrict__ signs,
                int32_t * __restrict__ dump, int units_per_wave, int n_tok) {
     using P = NbSpec<NB, NT>;
     static_assert(NT == 1 || (!DUMP && ROT == 0 && !GROUP), "small batch: plain GEMV only");
+    static_assert(!RP || (NT == 1 && !GROUP && !DUMP), "repacked layout: single-token GEMV only");
     static_assert(D >= 1 && D <= 3, "ring depth");
     static_assert(D * P::NPL < 64, "vmcnt range");
     static_assert(ROT == 0 || P::NCH % 32 == 0, "the rotation needs whole 1024-element blocks");
@@ -461,7 +468,7 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
 #pragma unroll
                 for (int r = 0; r < 16; ++r) v[r] *= sb[r];
             }
-            fwht1024_regs(v, lane);
+            if constexpr (ROT != 3) fwht1024_regs(v, lane);
             quant_pair_store(v, &act_lds[Q81_BYTES * (32 * b + (row >> 1))], row & 1);
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);        // lgkmcnt(0): this wave's LDS stores are done
@@ -503,6 +510,21 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
     const int sh = cw & 3;
     const int cw_al = cw - sh;
     const int dwo = PQ2_BYTES * (lane >> 2);
+    // repacked layout: slot j, lane l -> chunk c of row r of the unit; code
+    // unit at r*rowbytes + 2 nb + 8 ((c % 4) nb + c / 4), scale at
+    // r*rowbytes + 2 (c / 4)
+    int rp_code[RP ? P::S : 1], rp_dw[RP ? P::S : 1];
+    if constexpr (RP) {
+#pragma unroll
+        for (int j = 0; j < P::S; ++j) {
+            const int v = 64 * j + lane;
+            const int r = (P::G == 2 && v >= P::NCH) ? 1 : 0;
+            int c = v - r * P::NCH;
+            c = c < P::NCH ? c : 0;                        // idle lanes of a partial slot
+            rp_code[j] = r * PQ2_BYTES * NB + 2 * NB + 8 * ((c & 3) * NB + (c >> 2));
+            rp_dw[j] = r * PQ2_BYTES * NB + 2 * (c >> 2);
+        }
+    }
     float ykeep = 0.0f;                       // lane (G i + r) NT + t keeps row r, token t of unit i
 
     int i = 0;
@@ -524,10 +546,18 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         for (int t = 0; t < NT; ++t) acc0[t] = acc1[t] = 0.0f;
 #pragma unroll
         for (int j = 0; j < P::S; ++j) {
-            const uint32_t * cpa = reinterpret_cast<const uint32_t *>(ub + cw_al + SLOT_BYTES * j);
-            const uint32_t w0 = __builtin_amdgcn_alignbyte(cpa[1], cpa[0], sh);
-            const uint32_t w1 = __builtin_amdgcn_alignbyte(cpa[2], cpa[1], sh);
-            const uint32_t dwb = *reinterpret_cast<const uint16_t *>(ub + dwo + SLOT_BYTES * j);
+            uint32_t w0, w1, dwb;
+            if constexpr (RP) {
+                const uint2 wv = *reinterpret_cast<const uint2 *>(ub + rp_code[j]);
+                w0 = wv.x;
+                w1 = wv.y;
+                dwb = *reinterpret_cast<const uint16_t *>(ub + rp_dw[j]);
+            } else {
+                const uint32_t * cpa = reinterpret_cast<const uint32_t *>(ub + cw_al + SLOT_BYTES * j);
+                w0 = __builtin_amdgcn_alignbyte(cpa[1], cpa[0], sh);
+                w1 = __builtin_amdgcn_alignbyte(cpa[2], cpa[1], sh);
+                dwb = *reinterpret_cast<const uint16_t *>(ub + dwo + SLOT_BYTES * j);
+            }
             const bool second = (P::G == 2) && (j > P::SPLIT || (j == P::SPLIT && lane >= 32));
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
@@ -700,7 +730,7 @@ constexpr int nb_lds_bytes() {
     constexpr int act = (Q81_BYTES * P::NCH * NT + 1023) / 1024 * 1024;
     constexpr int ring = WAVES * (D + 1) * P::LDSB;
     constexpr int nhb = P::NCH / 32;
-    constexpr int stage = (ROT ? nhb * HBLK * 4 : 0) + (ROT == 2 ? nhb * HBLK * 4 : 0);
+    constexpr int stage = (ROT ? nhb * HBLK * 4 : 0) + (ROT == 2 ? nhb * HBLK * 4 : 0);   // ROT 3: x only
     return act + ring + stage;
 }
 
@@ -719,7 +749,7 @@ bool group_units(MatGroup & mg, int n_mat) {
     return u < 0x40000000;
 }
 
-template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, int NT = 1>
+template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, int NT = 1, bool RP = false>
 int launch_nb_t(MatGroup mg, int n_mat, const void * xin, const float * signs, int32_t * dump,
                 int per_cu, hipStream_t st, int n_tok = 1) {
     using P = NbSpec<NB, NT>;
@@ -739,7 +769,10 @@ int launch_nb_t(MatGroup mg, int n_mat, const void * xin, const float * signs, i
         upw = 64 / (P::G * NT);
         blocks = (n_units + upw * WAVES - 1) / (upw * WAVES);
     }
-    if constexpr (NT > 1)
+    if constexpr (RP)
+        hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, ROT, false, 1, true>), dim3(blocks),
+                           dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1);
+    else if constexpr (NT > 1)
         hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, 0, false, NT>), dim3(blocks), dim3(64 * WAVES),
                            0, st, mg, xin, signs, dump, upw, n_tok);
     else if (n_mat > 1)
@@ -1011,18 +1044,18 @@ int launch_nb_small_nt(const uint8_t * W, const uint8_t * X, float * Y, int n_ou
 // at 6144x5120 and 5120x6144, against 9.9 / 7.0 / 6.8 us for the pre-pass
 // plus the GEMV; two workgroups per CU: 6.9 us at 5120x6144), else 4 waves
 // with D = 2 or D = 1.  Returns -1 when no shape fits the LDS of a workgroup.
-template <int NB, int ROT>
+template <int NB, int ROT, bool RP = false>
 int launch_nb_rot(const MatGroup & mg, int n_mat, const float * x, const float * signs, hipStream_t st) {
     const int waves = env_int("BONSAI_FGEMV_WAVES", 8);
     int per_cu = env_int("BONSAI_GEMV_WG_PER_CU", 0);
     if (per_cu <= 0) per_cu = 1;
     if constexpr (nb_lds_bytes<NB, 2, 8, ROT>() <= LDS_PER_CU) {
-        if (waves == 8) return launch_nb_t<NB, 2, 8, false, ROT>(mg, n_mat, x, signs, nullptr, per_cu, st);
+        if (waves == 8) return launch_nb_t<NB, 2, 8, false, ROT, 1, RP>(mg, n_mat, x, signs, nullptr, per_cu, st);
     }
     if constexpr (nb_lds_bytes<NB, 2, 4, ROT>() <= LDS_PER_CU)
-        return launch_nb_t<NB, 2, 4, false, ROT>(mg, n_mat, x, signs, nullptr, per_cu, st);
+        return launch_nb_t<NB, 2, 4, false, ROT, 1, RP>(mg, n_mat, x, signs, nullptr, per_cu, st);
     else if constexpr (nb_lds_bytes<NB, 1, 4, ROT>() <= LDS_PER_CU)
-        return launch_nb_t<NB, 1, 4, false, ROT>(mg, n_mat, x, signs, nullptr, per_cu, st);
+        return launch_nb_t<NB, 1, 4, false, ROT, 1, RP>(mg, n_mat, x, signs, nullptr, per_cu, st);
     else
         return -1;
 }
@@ -1223,6 +1256,27 @@ int gemv_small_batch(const void * W, const void * Xq, float * Y, int64_t n_out, 
         case 80: return launch_nb_small_nt<80>(w, x, Y, (int)n_out, (int)n_tok, st);
         case 96: return launch_nb_small_nt<96>(w, x, Y, (int)n_out, (int)n_tok, st);
         case 136: return launch_nb_small_nt<136>(w, x, Y, (int)n_out, (int)n_tok, st);
+        default: return -1;
+    }
+}
+
+// Repacked-layout GEMV from fp32 x on the streaming kernel (quantised in
+// every workgroup, no rotation), for bonsai_p40_gemv_repack; -1 when the
+// width or alignment has no such kernel.
+int gemv_repack_streaming(const void * W, const float * x, float * y, int64_t n_out, int64_t n_in,
+                          bonsai_stream stream) {
+    if (n_out <= 0 || n_out > 0x3fffffff) return -1;
+    if (((uintptr_t)W & 15u) != 0 || ((uintptr_t)x & 15u) != 0) return -1;
+    if (env_int("BONSAI_GEMV_KERNEL", 0) != 0) return -1;
+    const MatGroup mg = single_group(W, y, n_out);
+    hipStream_t st = (hipStream_t)stream;
+    switch (n_in / QK_PQ2) {
+        case 8: return launch_nb_rot<8, 3, true>(mg, 1, x, nullptr, st);
+        case 40: return launch_nb_rot<40, 3, true>(mg, 1, x, nullptr, st);
+        case 48: return launch_nb_rot<48, 3, true>(mg, 1, x, nullptr, st);
+        case 80: return launch_nb_rot<80, 3, true>(mg, 1, x, nullptr, st);
+        case 96: return launch_nb_rot<96, 3, true>(mg, 1, x, nullptr, st);
+        case 136: return launch_nb_rot<136, 3, true>(mg, 1, x, nullptr, st);
         default: return -1;
     }
 }

@@ -145,6 +145,12 @@ int lds_limit() {
 
 }  // namespace
 
+namespace pq2 {
+// gemv.hip: the streaming kernel on the repacked layout; -1 if not applicable
+int gemv_repack_streaming(const void * W, const float * x, float * y, int64_t n_out, int64_t n_in,
+                          bonsai_stream stream);
+}
+
 extern "C" {
 
 int bonsai_p40_repack(const void * src, void * dst, int64_t n_out, int64_t n_in, bonsai_stream stream) {
@@ -171,6 +177,8 @@ int bonsai_p40_gemv_repack(const void * W, const float * x, float * y, int64_t n
     const int64_t nb = n_in / QK_PQ2;
     if (nb % 8 != 0 || n_out > 0x7fffffff) return 1;
     if (((uintptr_t)W & 7u) != 0) return 1;            // 8-byte units must be aligned
+    const int rc = pq2::gemv_repack_streaming(W, x, y, n_out, n_in, stream);
+    if (rc >= 0) return rc;
     const size_t lds = (size_t)nb * 4 * 40;
     if (lds > (size_t)lds_limit()) return 1;
     static bool attr_set = false;

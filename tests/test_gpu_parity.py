@@ -339,6 +339,32 @@ def test_repack_bytes_and_gemv_repack(n_out, n_in):
     assert normwise(host(y), O.gemv_repack(Wr_h, x, n_out, n_in)) <= TOL
 
 
+@pytest.mark.parametrize("n_out,n_in", [(17408, 5120), (5120, 17408), (6144, 5120), (17407, 5120),
+                                        (1023, 6144), (3, 1024), (100, 10240), (77, 12288)])
+def test_gemv_repack_streaming(n_out, n_in):
+    """The repacked-layout GEMV on the streaming kernel: against the oracle,
+    and bit-identical to bonsai_p40_gemv on the original layout with the
+    activation quantised by bonsai_p40_quant_activations (same chunk walk,
+    same quantiser, same sums)."""
+    case(f"gemv_repack streaming {n_out}x{n_in}")
+    W = O.gen_weights(1700 + n_out + n_in, n_out, n_in)
+    Wd = dev(W)
+    Wr = torch.zeros(W.size, dtype=torch.uint8, device="cuda")
+    B.repack(Wd, Wr, n_out, n_in)
+    x = O.gen_normal(1701 + n_in, n_in) * 1.3
+    xd = dev(x)
+    y = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+    B.gemv_repack(Wr, xd, y, n_out, n_in)
+    got = host(y)
+    assert np.all(np.isfinite(got))
+    assert normwise(got, O.gemv(W, O.quantize_q8_1(x, True), n_out, n_in, nthreads=16)) <= TOL
+    q = torch.zeros(n_in // 32 * 36, dtype=torch.uint8, device="cuda")
+    B.quant_activations(xd, q, n_in)
+    y2 = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+    B.gemv(Wd, q, y2, n_out, n_in)
+    np.testing.assert_array_equal(bits(got), bits(host(y2)))
+
+
 def test_repack_fixture(golden):
     case("repack fixture 8x5120")
     Wr = torch.zeros(golden["f4_5120_W"].size, dtype=torch.uint8, device="cuda")
