@@ -343,7 +343,7 @@ __device__ __forceinline__ float * rot_sign_stage() {
 template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, bool GROUP = false, int NT = 1, bool RP = false>
 __global__ void __launch_bounds__(64 * WAVES)
 gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * __restrict__ signs,
-               int32_t * __restrict__ dump, int units_per_wave, int n_tok) {
+               int32_t * __restrict__ dump, int units_per_wave, int n_tok, int xcd_log2m) {
     using P = NbSpec<NB, NT>;
     static_assert(NT == 1 || (!DUMP && ROT == 0 && !GROUP), "small batch: plain GEMV only");
     static_assert(!RP || (NT == 1 && !GROUP && !DUMP), "repacked layout: single-token GEMV only");
@@ -371,7 +371,18 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
     // slot-major wave numbering: the waves that carry one unit more than the
     // others are spread over all workgroups (hence all CUs) rather than packed
     // into the first ones
-    const int gw = wave * gridDim.x + blockIdx.x;
+    // XCD-aware numbering (xcd_log2m > 0, grid a multiple of 8 workgroups,
+    // which the dispatcher deals round-robin to the 8 XCDs): within a round
+    // of NW units, groups of M = 2^xcd_log2m consecutive units go to one XCD
+    // (its waves numbered wave-major), groups round-robin over the XCDs -- a
+    // line shared by two neighbouring units is then fetched into one L2.
+    int gw = wave * gridDim.x + blockIdx.x;
+    if (xcd_log2m > 0) {
+        const int K = gridDim.x >> 3;
+        const int t = wave * K + (blockIdx.x >> 3);
+        const int m = (1 << xcd_log2m) - 1;
+        gw = (((t >> xcd_log2m) << 3) + (blockIdx.x & 7)) << xcd_log2m | (t & m);
+    }
     const int NW = gridDim.x * WAVES;
     const int nu = gw < n_units ? min(units_per_wave, (n_units - 1 - gw) / NW + 1) : 0;
 
@@ -769,18 +780,22 @@ int launch_nb_t(MatGroup mg, int n_mat, const void * xin, const float * signs, i
         upw = 64 / (P::G * NT);
         blocks = (n_units + upw * WAVES - 1) / (upw * WAVES);
     }
+    // groups of 4 units per XCD: -3.4% HBM fetch and -3..5% time on the model's shapes
+    int xl = env_int("BONSAI_GEMV_XCD_LOG2M", 2);
+    if (xl < 0 || xl > 3 || blocks % 8 != 0) xl = 0;
+    while (xl > 0 && ((blocks / 8) * WAVES) % (1 << xl) != 0) --xl;
     if constexpr (RP)
         hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, ROT, false, 1, true>), dim3(blocks),
-                           dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1);
+                           dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl);
     else if constexpr (NT > 1)
         hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, 0, false, NT>), dim3(blocks), dim3(64 * WAVES),
-                           0, st, mg, xin, signs, dump, upw, n_tok);
+                           0, st, mg, xin, signs, dump, upw, n_tok, xl);
     else if (n_mat > 1)
         hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, DUMP, ROT, true>), dim3(blocks), dim3(64 * WAVES), 0,
-                           st, mg, xin, signs, dump, upw, 1);
+                           st, mg, xin, signs, dump, upw, 1, xl);
     else
         hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, DUMP, ROT, false>), dim3(blocks), dim3(64 * WAVES), 0,
-                           st, mg, xin, signs, dump, upw, 1);
+                           st, mg, xin, signs, dump, upw, 1, xl);
     return (int)hipGetLastError();
 }
 
