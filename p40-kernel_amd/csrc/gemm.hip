@@ -28,6 +28,7 @@
 #include "../../include/bonsai_p40.h"
 
 #include <stdlib.h>
+#include <type_traits>
 
 using namespace pq2;
 
@@ -663,14 +664,19 @@ int skinny_lds_limit() {
 // per output element (the int8 MFMA needs a convert and an FMA), and the
 // weight scale nothing beyond one packed f16 multiply per two staged codes.
 //
-// Workgroup: 512 threads (8 waves as 2 x 4), tile 128 rows x 128 tokens; a
-// wave owns 64 rows x 32 tokens = 4 x 2 MFMA tiles of 16 x 16.  Per PQ2_0
-// block (K = 128) the workgroup converts the tile's codes and Q8_1 bytes to
-// f16 once, into LDS laid out [chunk][row or token][32 positions] with the
-// four 16-byte groups of a row swizzled by (row / 4) % 4 (conflict-free
-// ds_read_b128 of the MFMA operands); the next block's raw bytes are loaded
-// into registers while the current block is computed, and two LDS stages
-// need one barrier per block.
+// Workgroup: tile 128 rows x 128 tokens, 1024 threads (16 waves as 4 x 4, 4
+// per SIMD; a wave owns 32 rows x 32 tokens = 2 x 2 MFMA tiles of 16 x 16) or
+// 512 (8 waves as 2 x 4, 64 x 32 each).  Per PQ2_0 block (K = 128) the
+// workgroup converts the tile's codes and Q8_1 bytes to f16 once, into LDS
+// laid out [chunk][row or token][32 positions] with the four 16-byte groups
+// of a row swizzled by (row / 4) % 4 (conflict-free ds_read_b128 of the MFMA
+// operands); the next block's raw bytes are loaded into registers while the
+// current block is computed, and two LDS stages need one barrier per block.
+//
+// A block scale with |dw| >= 32768 would overflow f16 at code 3 (2 dw): such
+// a block is staged as dw / 2 (exact there) and the workgroup repeats the
+// main loop once with every other block's scale set to 0, adding the second
+// half -- a second pass only for workgroups that meet such a scale.
 //
 // f16 conversions (exact):
 //  * code c -> f16(c - 1): v_perm picks the high byte from the table
@@ -678,7 +684,7 @@ int skinny_lds_limit() {
 //    v_perm spread 4 high bytes into 4 halves;
 //  * q -> f16(q): v_perm builds the halves 0x6400 + (q + 128) (= 1024 + q +
 //    128), a packed f16 add of -1152 leaves q.
-constexpr int GF_BM = 128, GF_BN = 128, GF_THREADS = 512;
+constexpr int GF_BM = 128, GF_BN = 128;
 constexpr int GF_STAGE_A = 4 * GF_BM * 64;          // bytes: [4 chunks][BM rows][64 B]
 constexpr int GF_STAGE_B = 4 * GF_BN * 64;
 
@@ -715,16 +721,29 @@ __device__ __forceinline__ void q4_to_f16(uint32_t q4, uint32_t & lo, uint32_t &
 // lanes per cycle) and with 64 banks (16 lanes per cycle).
 __device__ __forceinline__ int gf_swz(int r, int g) { return r * 64 + ((g ^ ((r >> 1) ^ (r >> 2))) & 3) * 16; }
 
-__global__ void __launch_bounds__(GF_THREADS)
+// WM x WN waves, each owning MI x NI MFMA tiles of 16 x 16 (the workgroup
+// tile is always 128 x 128).  With 512 threads every thread stages one A item
+// and one B item per block; with 1024 threads (4 waves per SIMD, for latency
+// hiding) waves 0-7 stage A items and waves 8-15 B items.
+template <int WM, int WN, int MI, int NI>
+__global__ void __launch_bounds__(64 * WM * WN)
 gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
                 float * __restrict__ Y, int n_out, int n_tok, int nb) {
+    constexpr int THREADS = 64 * WM * WN;
+    static_assert(16 * MI * WM == GF_BM && 16 * NI * WN == GF_BN, "workgroup tile");
+    static_assert(THREADS == 512 || THREADS == 1024, "staging roles");
+    constexpr bool SPLIT = THREADS == 1024;
     __shared__ __attribute__((aligned(16))) uint8_t sA[2][GF_STAGE_A];
     __shared__ __attribute__((aligned(16))) uint8_t sB[2][GF_STAGE_B];
     __shared__ __attribute__((aligned(16))) float sDa[2][4][GF_BN];
+    // set when a staged block scale was halved (below): the workgroup then
+    // runs a second pass over the halved blocks only
+    __shared__ int sHasBig;
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave & 1, wn = wave >> 1;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave % WM, wn = wave / WM;
     const int row0 = blockIdx.x * GF_BM, tok0 = blockIdx.y * GF_BN;
     const int l16 = lane & 15, g = lane >> 4;
     const size_t rs = (size_t)PQ2_BYTES * nb;                  // bytes per weight row
@@ -732,17 +751,40 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
 
     // staging roles: A item (row ar, chunk ap), B item (token bt, chunk bp);
     // LDS writes of a wave cover consecutive rows / tokens of one chunk
-    const int ar = tid & 127, ap = tid >> 7;                   // a wave stages 64 consecutive rows
-    const int bp = tid >> 7, bt = tid & 127;
+    const int it = tid & 511;
+    const int ar = it & 127, ap = it >> 7;                     // a wave stages 64 consecutive rows
+    const int bp = it >> 7, bt = it & 127;
     const bool a_ok = row0 + ar < n_out;
     const bool b_ok = tok0 + bt < n_tok;
 
+    float acc[MI][NI][4];
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[mi][ni][i] = 0.0f;
+
+    // the staging and main loop, specialised on the thread's staging roles
+    // (runtime role branches around the raw registers make the compiler keep
+    // them in scratch)
+    auto main_loop = [&](auto role_a, auto role_b) __attribute__((always_inline)) {
+    constexpr bool do_a = decltype(role_a)::value;
+    constexpr bool do_b = decltype(role_b)::value;
+    for (int pass = 0; pass < 2; ++pass) {
+    if (pass == 1) {                                           // rare: some |dw| >= 32768
+        __syncthreads();
+        if (!sHasBig) break;
+    }
     // raw bytes of one block held in registers between its global load and
     // its conversion into LDS; two sets, so a block's loads are issued two
-    // block-steps before they are consumed
+    // block-steps before they are consumed.  A: words 0-2 = 3-dword window
+    // over the 8 code bytes, word 3 = block scale; B: one Q8_1 block (9
+    // words), after A's words unless a thread stages only one of them.
+    constexpr int QB = do_a ? 4 : 0;
     struct Raw {
-        uint32_t a0, a1, a2, dw, sh;                           // A: 3-dword window, scale, shift (bit 3: block in range)
-        uint32_t q[9];                                         // B: one Q8_1 block
+        uint32_t w[QB + 9];
+        uint32_t sh;                                           // A: shift, bit 2 tail, bit 3 block in range
     };
     // byte offsets into W (kept as offsets so the loads stay global, not flat)
     const size_t w_align = (uintptr_t)W & 3;
@@ -754,20 +796,27 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
     // one, the conversion zeroes them) so the compiler can count them: the
     // wait before a conversion then leaves the younger block's loads in flight.
     auto prefetch = [&](Raw & r) {                             // the next block in order (the last block again past the end)
-        // dword-aligned window (in absolute address terms) over the 8 code bytes
-        const size_t aa = ((a_off + w_align) & ~(size_t)3) - w_align;
-        r.sh = (uint32_t)((a_off + w_align) & 3);
-        r.a0 = *reinterpret_cast<const uint32_t *>(W + aa);
-        r.a1 = *reinterpret_cast<const uint32_t *>(W + aa + 4);
-        // the window may end 2 bytes past W when its last byte is the matrix's
-        // last: then read the dword ending at W's end and shift (flag in sh bit 2)
-        const bool tail = aa + 12 > w_bytes;
-        r.a2 = *reinterpret_cast<const uint32_t *>(W + (tail ? aa + 6 : aa + 8));
-        r.sh |= (tail ? 4u : 0u) | (pf_block < nb ? 8u : 0u);
-        r.dw = (uint32_t)*reinterpret_cast<const uint16_t *>(W + a_off - 2 - 8 * ap);   // block scale
-        const uint32_t * xb = reinterpret_cast<const uint32_t *>(b_ptr);
+        if constexpr (do_a) {
+            // dword-aligned window (in absolute address terms) over the 8 code bytes
+            const size_t aa = ((a_off + w_align) & ~(size_t)3) - w_align;
+            r.sh = (uint32_t)((a_off + w_align) & 3);
+            r.w[0] = *reinterpret_cast<const uint32_t *>(W + aa);
+            r.w[1] = *reinterpret_cast<const uint32_t *>(W + aa + 4);
+            // the window may end 2 bytes past W when its last byte is the matrix's
+            // last: then read the dword ending at W's end and shift (flag in sh bit 2)
+            const bool tail = aa + 12 > w_bytes;
+            r.w[2] = *reinterpret_cast<const uint32_t *>(W + (tail ? aa + 6 : aa + 8));
+            r.sh |= (tail ? 4u : 0u) | (pf_block < nb ? 8u : 0u);
+            r.w[3] = (uint32_t)*reinterpret_cast<const uint16_t *>(W + a_off - 2 - 8 * ap);   // block scale
+        }
+        if constexpr (!do_a) {
+            r.sh = pf_block < nb ? 8u : 0u;
+        }
+        if constexpr (do_b) {
+            const uint32_t * xb = reinterpret_cast<const uint32_t *>(b_ptr);
 #pragma unroll
-        for (int k = 0; k < 9; ++k) r.q[k] = xb[k];
+            for (int k = 0; k < 9; ++k) r.w[QB + k] = xb[k];
+        }
         if (++pf_block < nb) {
             a_off += PQ2_BYTES;
             b_ptr += b_step;
@@ -776,48 +825,53 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
     // Conversion of one block's raw bytes into LDS stage st, in four parts
     // (part q writes 16-byte group q of every A and B row) so that it can be
     // interleaved with the four chunk steps of the current block.
-    uint32_t cw0, cw1;                                         // realigned code words
-    uint32_t dw2;                                              // the row's block scale, f16 x 2
+    uint32_t cw0 = 0, cw1 = 0;                                 // realigned code words
+    uint32_t dw2 = 0;                                          // the row's block scale, f16 x 2
     auto commit_part = [&](const Raw & r, int st, int q) {
-        if (q == 0) {
-            const uint32_t sh = r.sh & 3u;
-            const uint32_t a2 = (r.sh & 4u) ? (r.a2 >> 16) : r.a2;
-            cw0 = __builtin_amdgcn_alignbyte(r.a1, r.a0, sh);
-            cw1 = __builtin_amdgcn_alignbyte(a2, r.a1, sh);
-            cw0 = a_ok ? cw0 : 0x55555555u;                    // code 1 -> weight 0
-            cw1 = a_ok ? cw1 : 0x55555555u;
-            // a block past the end (the padding step of an odd block count) gets
-            // zero scales, so its products add exactly nothing
-            const bool live = (r.sh & 8u) != 0;
-            // the weight scale rides in A: (code - 1) * dw is exact in f16
-            // (code - 1 is -1, 0, 1 or 2); a dead row or block gets scale 0
-            const uint32_t dwh = (a_ok && live) ? (r.dw & 0xffffu) : 0u;
-            dw2 = dwh | (dwh << 16);
-            sDa[st][bp][bt] = (b_ok && live) ? f16_bits_to_f32(r.q[0] & 0xffffu) : 0.0f;
-        }
-        const uint32_t w = q < 2 ? cw0 : cw1;
-        const int k0 = 2 * (q & 1);                            // bit pair of position 8q
+        // a block past the end (the padding step of an odd block count) gets
+        // zero scales, so its products add exactly nothing
+        const bool live = (r.sh & 8u) != 0;
         uint32_t o0, o1, o2, o3;
-        codes4_to_f16((w >> (2 * k0)) & 0x03030303u, o0, o1);
-        codes4_to_f16((w >> (2 * k0 + 2)) & 0x03030303u, o2, o3);
-        o0 = mul_f16x2(o0, dw2); o1 = mul_f16x2(o1, dw2); o2 = mul_f16x2(o2, dw2); o3 = mul_f16x2(o3, dw2);
-        *reinterpret_cast<v4u *>(&sA[st][ap * GF_BM * 64] + gf_swz(ar, q)) = (v4u){o0, o1, o2, o3};
-        q4_to_f16(b_ok ? r.q[1 + 2 * q] : 0u, o0, o1);
-        q4_to_f16(b_ok ? r.q[2 + 2 * q] : 0u, o2, o3);
-        *reinterpret_cast<v4u *>(&sB[st][bp * GF_BN * 64] + gf_swz(bt, q)) = (v4u){o0, o1, o2, o3};
+        if constexpr (do_a) {
+            if (q == 0) {
+                const uint32_t sh = r.sh & 3u;
+                const uint32_t a2 = (r.sh & 4u) ? (r.w[2] >> 16) : r.w[2];
+                cw0 = __builtin_amdgcn_alignbyte(r.w[1], r.w[0], sh);
+                cw1 = __builtin_amdgcn_alignbyte(a2, r.w[1], sh);
+                cw0 = a_ok ? cw0 : 0x55555555u;                // code 1 -> weight 0
+                cw1 = a_ok ? cw1 : 0x55555555u;
+                // the weight scale rides in A: (code - 1) * dw is exact in f16
+                // (code - 1 is -1, 0, 1 or 2); a dead row or block gets scale 0.
+                // 2 * dw overflows f16 for |dw| >= 32768 (exponent field 30):
+                // such a block is staged with dw / 2 (exact there), which adds
+                // half of its
+                // contributions, once in the first pass and once more in a
+                // second pass that stages only those blocks (dw = 0 elsewhere)
+                uint32_t dwh = (a_ok && live) ? (r.w[3] & 0xffffu) : 0u;
+                const bool big = (dwh & 0x7C00u) == 0x7800u;
+                dwh -= big ? 0x400u : 0u;
+                dwh = (pass == 0 || big) ? dwh : 0u;
+                dw2 = dwh | (dwh << 16);
+                if (big) sHasBig = 1;
+            }
+            const uint32_t w = q < 2 ? cw0 : cw1;
+            const int k0 = 2 * (q & 1);                        // bit pair of position 8q
+            codes4_to_f16((w >> (2 * k0)) & 0x03030303u, o0, o1);
+            codes4_to_f16((w >> (2 * k0 + 2)) & 0x03030303u, o2, o3);
+            o0 = mul_f16x2(o0, dw2); o1 = mul_f16x2(o1, dw2); o2 = mul_f16x2(o2, dw2); o3 = mul_f16x2(o3, dw2);
+            *reinterpret_cast<v4u *>(&sA[st][ap * GF_BM * 64] + gf_swz(ar, q)) = (v4u){o0, o1, o2, o3};
+        }
+        if constexpr (do_b) {
+            if (q == 0) sDa[st][bp][bt] = (b_ok && live) ? f16_bits_to_f32(r.w[QB] & 0xffffu) : 0.0f;
+            q4_to_f16(b_ok ? r.w[QB + 1 + 2 * q] : 0u, o0, o1);
+            q4_to_f16(b_ok ? r.w[QB + 2 + 2 * q] : 0u, o2, o3);
+            *reinterpret_cast<v4u *>(&sB[st][bp * GF_BN * 64] + gf_swz(bt, q)) = (v4u){o0, o1, o2, o3};
+        }
     };
     auto commit = [&](const Raw & r, int st) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) commit_part(r, st, q);
     };
-
-    float acc[4][2][4];
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[mi][ni][i] = 0.0f;
 
     Raw raw0, raw1;
     prefetch(raw0);
@@ -835,41 +889,41 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
         // chunk pipeline: the MFMAs of chunk p+1 are issued before the epilogue
         // of chunk p, and a quarter of the next block's conversion follows each
         // epilogue, so VALU work runs while the matrix core is busy
-        v4f S[2][4][2];
-        float da[2][2];
+        v4f S[2][MI][NI];
+        float da[2][NI];
         auto issue = [&](int p) {
             const uint8_t * a_src = &sA[st][p * GF_BM * 64];
             const uint8_t * b_src = &sB[st][p * GF_BN * 64];
-            v8h A[4], Bf[2];
+            v8h A[MI], Bf[NI];
 #pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
-                A[mi] = *reinterpret_cast<const v8h *>(a_src + gf_swz(wm * 64 + 16 * mi + l16, g));
+            for (int mi = 0; mi < MI; ++mi)
+                A[mi] = *reinterpret_cast<const v8h *>(a_src + gf_swz(wm * 16 * MI + 16 * mi + l16, g));
 #pragma unroll
-            for (int ni = 0; ni < 2; ++ni) {
-                const int tt = wn * 32 + 16 * ni + l16;
+            for (int ni = 0; ni < NI; ++ni) {
+                const int tt = wn * 16 * NI + 16 * ni + l16;
                 Bf[ni] = *reinterpret_cast<const v8h *>(b_src + gf_swz(tt, g));
                 da[p & 1][ni] = sDa[st][p][tt];
             }
 #pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
+            for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-                for (int ni = 0; ni < 2; ++ni)
+                for (int ni = 0; ni < NI; ++ni)
                     S[p & 1][mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mi], Bf[ni], (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
         };
         auto epilogue = [&](int p) {
 #pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
+            for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-                for (int ni = 0; ni < 2; ++ni)
+                for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
                         acc[mi][ni][i] = fmaf(da[p & 1][ni], S[p & 1][mi][ni][i], acc[mi][ni][i]);
             // pin the chunk's epilogue here: without it the compiler sinks all
             // the FMAs below the last MFMA and keeps every result live
 #pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
+            for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-                for (int ni = 0; ni < 2; ++ni)
+                for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[mi][ni][i]));
         };
@@ -885,20 +939,30 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
         }
         __syncthreads();
     };
+
     // register sets alternate; an odd block count runs one padding step whose
     // scales are zero
     for (int b = 0; b < nb; b += 2) {
         step(b, raw0, raw1);
         step(b + 1, raw1, raw0);
     }
+    }
+    };
+    using yes = std::integral_constant<bool, true>;
+    using no = std::integral_constant<bool, false>;
+    if (tid == 0) sHasBig = 0;
+    __syncthreads();
+    if constexpr (!SPLIT) main_loop(yes{}, yes{});
+    else if (wave < 8) main_loop(yes{}, no{});
+    else main_loop(no{}, yes{});
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
-            const int tok = tok0 + wn * 32 + 16 * ni + l16;
+        for (int ni = 0; ni < NI; ++ni) {
+            const int tok = tok0 + wn * 16 * NI + 16 * ni + l16;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int row = row0 + wm * 64 + 16 * mi + 4 * g + i;
+                const int row = row0 + wm * 16 * MI + 16 * mi + 4 * g + i;
                 if (row < n_out && tok < n_tok) Y[(size_t)row * n_tok + tok] = acc[mi][ni][i];
             }
         }
@@ -956,7 +1020,13 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
     }
     if (env_int_gemm("BONSAI_GEMM_KERNEL", 0) == 0) {
         dim3 grid((unsigned)cdiv(n_out, GF_BM), (unsigned)cdiv(n_tok, GF_BN));
-        hipLaunchKernelGGL(gemm_f16_kernel, grid, dim3(GF_THREADS), 0, st, w, x, Y, (int)n_out, (int)n_tok, nb);
+        // 16 waves (4 per SIMD, 32 x 32 wave tiles) measured 12-22 % faster than
+        // 8 waves (2 per SIMD, 64 x 32) on every prefill shape: the latency of
+        // the chunk pipeline and the per-block barrier is hidden by more waves
+        if (env_int_gemm("BONSAI_GEMM_F16_WAVES", 16) == 8)
+            hipLaunchKernelGGL((gemm_f16_kernel<2, 4, 4, 2>), grid, dim3(512), 0, st, w, x, Y, (int)n_out, (int)n_tok, nb);
+        else
+            hipLaunchKernelGGL((gemm_f16_kernel<4, 4, 2, 2>), grid, dim3(1024), 0, st, w, x, Y, (int)n_out, (int)n_tok, nb);
     } else if ((nb & 1) || ((uintptr_t)W & 3u) != 0) {
         dim3 grid((unsigned)cdiv(n_out, 64), (unsigned)cdiv(n_tok, 64));
         hipLaunchKernelGGL(gemm_mfma_kernel_u16, grid, dim3(256), 0, st, w, x, Y, (int)n_out, (int)n_tok, nb);

@@ -484,6 +484,40 @@ def test_gemm_subnormal_and_zero_block_scales():
     assert normwise(host(Y), O.gemm(W, Xq, n_out, n_in, n_tok, nthreads=16)) <= TOL
 
 
+@pytest.mark.parametrize("waves", ["16", "8"])
+def test_gemm_large_block_scales_with_code3(waves, monkeypatch):
+    """Blocks whose fp16 scale has |d| >= 32768 and that hold code 3 (value
+    2d, past the fp16 range): the prefill kernel stages d / 2 for them and
+    doubles their chunk sums; both workgroup shapes, and the GEMV on the same
+    weights."""
+    monkeypatch.setenv("BONSAI_GEMM_F16_WAVES", waves)
+    case(f"gemm 200x2048x64 with |d| >= 32768 and code 3 ({waves} waves)")
+    n_out, n_in, n_tok = 200, 2048, 64
+    W = O.gen_weights(1700, n_out, n_in).copy()
+    nb = n_in // 128
+    rng = np.random.default_rng(17)
+    for r in range(n_out):
+        for b in rng.choice(nb, 3 if r % 5 else 0, replace=False):
+            off = (r * nb + b) * 34
+            bits = np.uint16(rng.integers(0x7800, 0x7C00) | (0x8000 if rng.random() < 0.5 else 0))
+            W[off:off + 2] = np.frombuffer(bits.tobytes(), np.uint8)
+            W[off + 2:off + 34] = rng.integers(0, 256, 32, dtype=np.uint8)
+    _, codes = O.pq2_fields(W)
+    assert np.any(codes == 3)
+    X = O.gen_normal(1701, n_tok * n_in).reshape(n_tok, n_in)
+    Xq = O.quantize_chunk_major(X)
+    Y = torch.full((n_out, n_tok), float("nan"), dtype=torch.float32, device="cuda")
+    Wd = dev(W)
+    B.gemm(Wd, dev(Xq), Y, n_out, n_in, n_tok)
+    got = host(Y)
+    assert np.all(np.isfinite(got))
+    assert normwise(got, O.gemm(W, Xq, n_out, n_in, n_tok, nthreads=16)) <= TOL
+    xq = O.quantize_q8_1(X[0], True)
+    y = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+    B.gemv(Wd, dev(xq), y, n_out, n_in)
+    assert normwise(host(y), O.gemv(W, xq, n_out, n_in)) <= TOL
+
+
 def test_gemm_equals_gemv_per_token():
     case("gemm n_tok=3 equals three gemv")
     n_out, n_in, n_tok = 300, 5120, 3
