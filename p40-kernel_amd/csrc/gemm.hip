@@ -754,8 +754,6 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
     const int it = tid & 511;
     const int ar = it & 127, ap = it >> 7;                     // a wave stages 64 consecutive rows
     const int bp = it >> 7, bt = it & 127;
-    const bool a_ok = row0 + ar < n_out;
-    const bool b_ok = tok0 + bt < n_tok;
 
     float acc[MI][NI][4];
 #pragma unroll
@@ -836,10 +834,10 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
             if (q == 0) {
                 const uint32_t sh = r.sh & 3u;
                 const uint32_t a2 = (r.sh & 4u) ? (r.w[2] >> 16) : r.w[2];
+                // rows past n_out (re-reading the last row) only reach their
+                // own outputs, which are not stored
                 cw0 = __builtin_amdgcn_alignbyte(r.w[1], r.w[0], sh);
                 cw1 = __builtin_amdgcn_alignbyte(a2, r.w[1], sh);
-                cw0 = a_ok ? cw0 : 0x55555555u;                // code 1 -> weight 0
-                cw1 = a_ok ? cw1 : 0x55555555u;
                 // the weight scale rides in A: (code - 1) * dw is exact in f16
                 // (code - 1 is -1, 0, 1 or 2); a dead row or block gets scale 0.
                 // 2 * dw overflows f16 for |dw| >= 32768 (exponent field 30):
@@ -847,7 +845,7 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
                 // half of its
                 // contributions, once in the first pass and once more in a
                 // second pass that stages only those blocks (dw = 0 elsewhere)
-                uint32_t dwh = (a_ok && live) ? (r.w[3] & 0xffffu) : 0u;
+                uint32_t dwh = live ? (r.w[3] & 0xffffu) : 0u;
                 const bool big = (dwh & 0x7C00u) == 0x7800u;
                 dwh -= big ? 0x400u : 0u;
                 dwh = (pass == 0 || big) ? dwh : 0u;
@@ -862,9 +860,11 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
             *reinterpret_cast<v4u *>(&sA[st][ap * GF_BM * 64] + gf_swz(ar, q)) = (v4u){o0, o1, o2, o3};
         }
         if constexpr (do_b) {
-            if (q == 0) sDa[st][bp][bt] = (b_ok && live) ? f16_bits_to_f32(r.w[QB] & 0xffffu) : 0.0f;
-            q4_to_f16(b_ok ? r.w[QB + 1 + 2 * q] : 0u, o0, o1);
-            q4_to_f16(b_ok ? r.w[QB + 2 + 2 * q] : 0u, o2, o3);
+            // tokens past n_tok (re-reading the last token) only reach their
+            // own output columns, which are not stored
+            if (q == 0) sDa[st][bp][bt] = live ? f16_bits_to_f32(r.w[QB] & 0xffffu) : 0.0f;
+            q4_to_f16(r.w[QB + 1 + 2 * q], o0, o1);
+            q4_to_f16(r.w[QB + 2 + 2 * q], o2, o3);
             *reinterpret_cast<v4u *>(&sB[st][bp * GF_BN * 64] + gf_swz(bt, q)) = (v4u){o0, o1, o2, o3};
         }
     };
