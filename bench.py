@@ -187,6 +187,21 @@ def bench_prepass(n, steps, warmup, gen):
     return time_loop(lambda i: B.fwht_quant(x, None, q, n), steps, warmup)
 
 
+def bench_rms_prepass(n, steps, warmup, gen):
+    """Layer-input pre-pass: bonsai_p40_rmsnorm_fwht_quant (one launch) and
+    the unfused bonsai_p40_rmsnorm + bonsai_p40_fwht_quant (two launches)."""
+    x = torch.randn(n, generator=gen, device="cuda")
+    w = torch.randn(n, generator=gen, device="cuda") * 0.1 + 1
+    h = torch.empty(n, dtype=torch.float32, device="cuda")
+    q = torch.empty(B.q8_bytes(n), dtype=torch.uint8, device="cuda")
+    fused = time_loop(lambda i: B.rmsnorm_fwht_quant(x, w, None, q, n, 1, 1e-6), steps, warmup)
+
+    def two(i):
+        B.rmsnorm(x, w, h, 1, n, 1e-6)
+        B.fwht_quant(h, None, q, n)
+    return fused, time_loop(two, steps, warmup)
+
+
 def bench_ffn_chain(steps, warmup, gen):
     """Config 1: pre-pass, gate + up GEMVs, SwiGLU+FWHT+Q8_1, down GEMV."""
     sets = []
@@ -399,6 +414,11 @@ def main():
         for n in (N_EMBD, N_FF):
             m = bench_prepass(n, args.steps, args.warmup, gen)
             extra[f"fwht_quant_{n}_us"] = round(m * 1e3, 3)
+            mf, m2 = bench_rms_prepass(n, args.steps, args.warmup, gen)
+            extra[f"rmsnorm_fwht_quant_{n}"] = {"us": round(mf * 1e3, 3), "unfused_us": round(m2 * 1e3, 3),
+                                                "note": "fused RMSNorm+FWHT+Q8_1 vs rmsnorm then fwht_quant"}
+            print(f"[bench] rmsnorm_fwht_quant {n}: {extra[f'rmsnorm_fwht_quant_{n}']}", file=sys.stderr,
+                  flush=True)
         for (n_out, n_in) in ((N_FF, N_EMBD), (N_EMBD, N_FF)):
             m = bench_gemv_repack(n_out, n_in, args.steps, args.warmup, gen)
             extra[f"gemv_repack_{n_out}x{n_in}"] = {

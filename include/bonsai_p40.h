@@ -112,6 +112,19 @@ int bonsai_p40_fwht_quant(const float * x, const float * signs, void * xq, int64
 int bonsai_p40_quant_tokens(const float * X, const float * signs, void * Xq, int64_t n,
                             int64_t n_tok, int rotate, bonsai_stream stream);
 
+// Layer-input pre-pass: Xq = Q8_1(FWHT(signs .* RMSNorm(x, w, eps))) for n_tok
+// token rows of n floats, one launch in place of bonsai_p40_rmsnorm followed by
+// bonsai_p40_fwht and bonsai_p40_quant_activations (elementwise_p40.cu:17-41,
+// 48-88 + gemv_p40.cu:168-196; RMSNorm as src/ops.h:13-22).  The sum of squares
+// is accumulated in fp64, so the scale can differ from the reference's
+// sequential fp32 sum by that sum's rounding; the rest is bit-identical to the
+// host FWHT and quantiser.  Output chunk-major (block (c, t) at c*n_tok + t: the
+// GEMM's Xq; for n_tok == 1 the GEMV's xq).  x, w and signs are [n_tok][n], [n]
+// and [n] (signs may be NULL).  Errors: 1 if n <= 0, n % 1024 != 0, x or w is
+// NULL, or xq is not 4-byte aligned; 0 (no-op) if n_tok <= 0.
+int bonsai_p40_rmsnorm_fwht_quant(const float * x, const float * w, const float * signs, void * xq,
+                                  int64_t n, int64_t n_tok, float eps, bonsai_stream stream);
+
 // FFN glue of the decode chain: xq = Q8_1(FWHT(signs .* (silu(gate) * up)))
 // with silu(g) = g / (1 + exp(-g)) (src/ops.h:27-31), one launch.
 // Errors: 1 if n <= 0 or n % 1024 != 0.

@@ -69,6 +69,7 @@ def lib():
         L.orc_repack_row_dot.argtypes = [_u8p, _u8p, _i64]; L.orc_repack_row_dot.restype = C.c_float
         L.orc_gemv_repack.argtypes = [_u8p, _f32p, _f32p, _i64, _i64, C.c_int]
         L.orc_swiglu.argtypes = [_f32p, _f32p, _f32p, _i64]
+        L.orc_rmsnorm.argtypes = [_f32p, _f32p, _f32p, _i64, C.c_float]
         L.orc_gen_normal.argtypes = [C.c_uint64, _f32p, _i64, C.c_float]
         L.orc_gen_weights.argtypes = [C.c_uint64, _u8p, _i64, _i64, C.c_double]
     return _lib
@@ -97,6 +98,7 @@ def ref():
         R.ref_unpack_rows.argtypes = [_u8p, _u8p, _i64, _i64]; R.ref_unpack_rows.restype = C.c_int
         R.ref_repack_row_dot.argtypes = [_u8p, _u8p, _i64]; R.ref_repack_row_dot.restype = C.c_float
         R.ref_swiglu.argtypes = [_f32p, _f32p, _f32p, _i64]
+        R.ref_rmsnorm.argtypes = [_f32p, _f32p, _f32p, _i64, C.c_float]
     return _ref
 
 
@@ -192,6 +194,14 @@ def swiglu(g: np.ndarray, u: np.ndarray) -> np.ndarray:
     g = np.ascontiguousarray(g, np.float32); u = np.ascontiguousarray(u, np.float32)
     y = np.empty_like(g)
     lib().orc_swiglu(_p(g, _f32p), _p(u, _f32p), _p(y, _f32p), g.size)
+    return y
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """RMSNorm of one row (src/ops.h:13-22): sequential fp32 sum of squares."""
+    x = np.ascontiguousarray(x, np.float32); w = np.ascontiguousarray(w, np.float32)
+    y = np.empty_like(x)
+    lib().orc_rmsnorm(_p(x, _f32p), _p(w, _f32p), _p(y, _f32p), x.size, C.c_float(eps))
     return y
 
 

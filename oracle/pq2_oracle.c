@@ -21,6 +21,7 @@
  *   orc_repack_*        -- F5 fixtures + round trip
  *   orc_gemm            -- F6 fixtures + double-precision dequantised reference
  *   orc_swiglu          -- F7 fixtures (chain) within expf ulp tolerance
+ *   orc_rmsnorm         -- F8 fixtures (bit patterns) + float64 closed form
  */
 #include <math.h>
 #include <stdint.h>
@@ -341,6 +342,16 @@ void orc_gemv_repack(const uint8_t *Wr, const float *x, float *y, int64_t n_out,
 /* ---- SwiGLU: src/ops.h:27-31 (silu(g) = g / (1 + expf(-g))) ----------- */
 void orc_swiglu(const float *g, const float *u, float *y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+}
+
+/* ---- RMSNorm: src/ops.h:13-22 ------------------------------------------
+ * s = 1 / sqrtf(ss / n + eps) with ss the sequential fp32 sum of x[i]^2
+ * (each square and each addition rounded), then y = (x * s) * w. */
+void orc_rmsnorm(const float *x, const float *w, float *y, int64_t n, float eps) {
+    float ss = 0.0f;
+    for (int64_t i = 0; i < n; ++i) ss += x[i] * x[i];
+    const float s = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int64_t i = 0; i < n; ++i) y[i] = x[i] * s * w[i];
 }
 
 /* ---- seeded synthetic inputs (own generator: splitmix64 + Box-Muller) --- */

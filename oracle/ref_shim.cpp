@@ -93,5 +93,6 @@ float ref_repack_row_dot(const void * row, const void * act, int64_t nb) {
 }
 
 void ref_swiglu(const float * g, const float * u, float * y, int64_t n) { swiglu(g, u, y, (int)n); }
+void ref_rmsnorm(const float * x, const float * w, float * y, int64_t n, float eps) { rmsnorm(x, w, y, (int)n, eps); }
 
 }  // extern "C"

@@ -39,6 +39,7 @@ SIGNATURES = {
     "bonsai_p40_fwht_quant": [_F32P, _F32P, _V, _I64, _V],
     "bonsai_p40_quant_tokens": [_F32P, _F32P, _V, _I64, _I64, C.c_int, _V],
     "bonsai_p40_swiglu_fwht_quant": [_F32P, _F32P, _F32P, _V, _I64, _V],
+    "bonsai_p40_rmsnorm_fwht_quant": [_F32P, _F32P, _F32P, _V, _I64, _I64, C.c_float, _V],
     "bonsai_p40_fwht_gemv": [_V, _F32P, _F32P, _F32P, _I64, _I64, _V],
     "bonsai_p40_gemv_group": [_V, _V, _V, C.c_int, _V, _I64, _V],
     "bonsai_p40_fwht_gemv_group": [_V, _V, _V, C.c_int, _F32P, _F32P, _I64, _V],
@@ -141,6 +142,12 @@ def quant_tokens(X, signs, Xq, n: int, n_tok: int, rotate: bool, stream=None) ->
 def swiglu_fwht_quant(gate, up, signs, xq, n: int, stream=None) -> None:
     _check("bonsai_p40_swiglu_fwht_quant",
            call("bonsai_p40_swiglu_fwht_quant", gate, up, signs, xq, n, stream=stream))
+
+
+def rmsnorm_fwht_quant(x, w, signs, xq, n: int, n_tok: int, eps: float, stream=None) -> None:
+    _check("bonsai_p40_rmsnorm_fwht_quant",
+           call("bonsai_p40_rmsnorm_fwht_quant", x, w, signs, xq, n, n_tok, C.c_float(eps),
+                stream=stream))
 
 
 def fwht_gemv(W, x, signs, y, n_out: int, n_in: int, stream=None) -> None:

@@ -3,7 +3,9 @@
 //   * permuted Q8_1 quantisation with the reference host rounding,
 //   * both fused into one LDS-resident butterfly kernel, optionally preceded
 //     by SwiGLU (the FFN glue) and writing the GEMV (token-major) or the GEMM
-//     (chunk-major) activation layout.
+//     (chunk-major) activation layout;
+//   * RMSNorm -> FWHT -> Q8_1 of token rows in one launch (the step before
+//     every projection of a layer).
 //
 // Reference semantics: src/fwht.h:20-42 (transform, stage order, signs of
 // length n), src/pq2_0.h:99-126 (quantiser), src/ops.h:27-31 (SwiGLU); device
@@ -94,6 +96,113 @@ quant_kernel(const float * __restrict__ x, uint8_t * __restrict__ q, int nchunk,
     quant_pair_store(v, q + bidx * Q81_BYTES, half);
 }
 
+// RMSNorm -> FWHT -> Q8_1 of token rows (src/ops.h:13-22, then the pre-pass
+// above).  Grid n_tok, one workgroup per token, nw = min(n / 1024, 16) waves;
+// wave w owns the Hadamard blocks w, w + nw, ...  The sum of squares is
+// accumulated in fp64 (every fp32 square is exact there, and the rounding of
+// the fp64 sum sits far below fp32's), so s = 1 / sqrtf((float)(ss / n) + eps)
+// does not depend on the reduction order; the reference's sequential fp32 sum
+// differs from it by that sum's own rounding.  Then y = (x * s) * w, the
+// signs, the register FWHT and the quantiser, as the pre-pass.  Output
+// chunk-major (block (c, t) at c * n_tok + t; for one token the GEMV layout).
+template <bool VEC, bool SIGNS>
+__global__ void __launch_bounds__(1024)
+rms_rot_quant_kernel(const float * __restrict__ x, const float * __restrict__ w,
+                     const float * __restrict__ signs, uint8_t * __restrict__ q, int n, int n_tok,
+                     float eps) {
+    __shared__ double red[16];
+    const int l = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int tok = blockIdx.x;
+    const int nhb = n / HBLK;
+    const int row = fwht_row(l);
+    const float * xt = x + (size_t)tok * n;
+
+    double ss = 0.0;
+    for (int b = wave; b < nhb; b += nw) {
+        float v[16];
+        load16(xt + (size_t)HBLK * b + 16 * row, v, VEC);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ss += (double)v[r] * (double)v[r];
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    if (l == 0) red[wave] = ss;
+    __syncthreads();
+    double tot = 0.0;
+    for (int i = 0; i < nw; ++i) tot += red[i];
+    const float s = 1.0f / sqrtf((float)(tot / (double)n) + eps);
+
+    for (int b = wave; b < nhb; b += nw) {
+        float v[16], wv[16];
+        load16(xt + (size_t)HBLK * b + 16 * row, v, VEC);
+        load16(w + (size_t)HBLK * b + 16 * row, wv, VEC);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v[r] = v[r] * s * wv[r];
+        if constexpr (SIGNS) {
+            float sg[16];
+            load16(signs + (size_t)HBLK * b + 16 * row, sg, VEC);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) v[r] *= sg[r];
+        }
+        fwht1024_regs(v, l);
+        const size_t c = (size_t)b * (HBLK / QK8) + (row >> 1);
+        quant_pair_store(v, q + (c * n_tok + tok) * Q81_BYTES, row & 1);
+    }
+}
+
+// The same, one workgroup (4 waves) per (Hadamard block, token) for few
+// tokens: every workgroup computes the token's sum of squares itself, with
+// the same code and the same thread-to-element order (so all blocks of a
+// token get a bit-identical scale), while wave 0's own block of x, w and
+// signs is already in flight; wave 0 then normalises, rotates and quantises.
+// The whole row is read once per block (an L2 hit after the first): the
+// blocks spread over the CUs instead of queueing on one.
+template <bool VEC, bool SIGNS>
+__global__ void __launch_bounds__(256)
+rms_rot_quant_block_kernel(const float * __restrict__ x, const float * __restrict__ w,
+                           const float * __restrict__ signs, uint8_t * __restrict__ q, int n,
+                           int n_tok, float eps) {
+    __shared__ double red[4];
+    const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
+    const int b = blockIdx.x, tok = blockIdx.y;
+    const int row = fwht_row(l);
+    const float * xt = x + (size_t)tok * n;
+    float v[16], wv[16], sg[16];
+    if (wave == 0) {
+        load16(xt + (size_t)HBLK * b + 16 * row, v, VEC);
+        load16(w + (size_t)HBLK * b + 16 * row, wv, VEC);
+        if constexpr (SIGNS) load16(signs + (size_t)HBLK * b + 16 * row, sg, VEC);
+    }
+    double ss = 0.0;
+    if constexpr (VEC) {
+        const float4 * x4 = reinterpret_cast<const float4 *>(xt);
+        for (int i = tid; i < n / 4; i += 256) {
+            const float4 t = x4[i];
+            ss += (double)t.x * (double)t.x + (double)t.y * (double)t.y;
+            ss += (double)t.z * (double)t.z + (double)t.w * (double)t.w;
+        }
+    } else {
+        for (int i = tid; i < n; i += 256) ss += (double)xt[i] * (double)xt[i];
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    if (l == 0) red[wave] = ss;
+    __syncthreads();
+    if (wave != 0) return;
+    const double tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float s = 1.0f / sqrtf((float)(tot / (double)n) + eps);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[r] = v[r] * s * wv[r];
+    if constexpr (SIGNS) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v[r] *= sg[r];
+    }
+    fwht1024_regs(v, l);
+    const size_t c = (size_t)b * (HBLK / QK8) + (row >> 1);
+    quant_pair_store(v, q + (c * n_tok + tok) * Q81_BYTES, row & 1);
+}
+
 inline bool al16(const void * p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 inline bool al4(const void * p) { return ((uintptr_t)p & 3u) == 0; }
 
@@ -162,6 +271,32 @@ int bonsai_p40_quant_tokens(const float * X, const float * signs, void * Xq, int
                                                             (hipStream_t)stream);
     if (signs != nullptr) return 1;   // signs only apply with the rotation
     return launch_quant(X, Xq, n, n_tok, true, (hipStream_t)stream);
+}
+
+int bonsai_p40_rmsnorm_fwht_quant(const float * x, const float * w, const float * signs, void * xq,
+                                  int64_t n, int64_t n_tok, float eps, bonsai_stream stream) {
+    if (n <= 0 || n % HBLK != 0 || x == nullptr || w == nullptr || !al4(xq)) return 1;
+    if (n_tok <= 0) return 0;
+    if (n_tok > 0x7fffffff || n > 0x7fffffff) return 1;
+    const int nw = (int)(n / HBLK < 16 ? n / HBLK : 16);
+    const bool vec = al16(x) && al16(w) && al16(signs);
+    hipStream_t st = (hipStream_t)stream;
+    // few tokens: a workgroup per block (spread over the CUs); many: one per
+    // token (each token row read once)
+    const bool per_block = n_tok * (n / HBLK) <= 4096 && n_tok <= 65535 && n / HBLK <= 0x7fffffff;
+#define PQ2_RMS_LAUNCH(V, S)                                                                        \
+    if (per_block)                                                                                  \
+        hipLaunchKernelGGL((rms_rot_quant_block_kernel<V, S>), dim3((unsigned)(n / HBLK), (unsigned)n_tok), \
+                           dim3(256), 0, st, x, w, signs, (uint8_t *)xq, (int)n, (int)n_tok, eps);  \
+    else                                                                                            \
+        hipLaunchKernelGGL((rms_rot_quant_kernel<V, S>), dim3((unsigned)n_tok), dim3(64 * nw), 0, st, \
+                           x, w, signs, (uint8_t *)xq, (int)n, (int)n_tok, eps)
+    if (vec && signs) PQ2_RMS_LAUNCH(true, true);
+    else if (vec) PQ2_RMS_LAUNCH(true, false);
+    else if (signs) PQ2_RMS_LAUNCH(false, true);
+    else PQ2_RMS_LAUNCH(false, false);
+#undef PQ2_RMS_LAUNCH
+    return (int)hipGetLastError();
 }
 
 int bonsai_p40_swiglu_fwht_quant(const float * gate, const float * up, const float * signs,

@@ -1,4 +1,4 @@
-"""Writes the golden fixtures F1-F7 from the reference's own host code.
+"""Writes the golden fixtures F1-F8 from the reference's own host code.
 
 The vectors come from oracle/_ref/libbonsai_ref.so, i.e. the reference
 headers src/pq2_0.h, src/fwht.h, src/pq2_0_repack.h and src/ops.h compiled
@@ -159,6 +159,17 @@ def main():
     R.ref_swiglu(p(g, O._f32p), p(u, O._f32p), p(h, O._f32p), 2048)
     fx["f7_gate"], fx["f7_up"], fx["f7_h"] = g, u, h
     fx["f7_hq"] = ref_q8(R, ref_fwht(R, h), True)
+
+    # F8: RMSNorm (src/ops.h:13-22) -> FWHT -> Q8_1, two rows and two eps
+    for (n, seed, eps) in ((3072, 111, 1e-6), (1024, 113, 1e-2)):
+        x = O.gen_normal(seed, n) * 3
+        w = O.gen_normal(seed + 1, n) * 0.1 + 1
+        y = np.empty(n, np.float32)
+        R.ref_rmsnorm(p(x, O._f32p), p(w, O._f32p), p(y, O._f32p), n, C.c_float(eps))
+        tag = f"f8_{n}"
+        fx[tag + "_x"], fx[tag + "_w"], fx[tag + "_y"] = x, w, y
+        fx[tag + "_eps"] = np.float32(eps)
+        fx[tag + "_yq"] = ref_q8(R, ref_fwht(R, y), True)
 
     np.savez_compressed(OUT, **fx)
     print(f"wrote {OUT}: {os.path.getsize(OUT)} bytes, {len(fx)} arrays")

@@ -575,6 +575,82 @@ def test_ffn_chain_config1():
     assert normwise(host(y), O.gemv(Wd, hq_full, n_embd, n_ff, 16)) <= 2e-3
 
 
+# ------------------------------------------- RMSNorm -> FWHT -> Q8_1 pre-pass
+def rms_scale_fp64(x: np.ndarray, eps: float) -> np.float32:
+    """The fused kernel's scale: fp64 sum of the (exact) squares, then
+    1 / sqrtf(float(ss / n) + eps) in fp32 (each step correctly rounded)."""
+    ss = np.sum(x.astype(np.float64) ** 2)
+    m = np.float32(ss / x.size)
+    return np.float32(1.0) / np.sqrt(np.float32(m + np.float32(eps)))
+
+
+def chunk_major(blocks):
+    """Token-major Q8_1 rows -> chunk-major (block (c, t) at c * n_tok + t)."""
+    B_ = np.stack([b.reshape(-1, 36) for b in blocks], axis=1)
+    return B_.reshape(-1)
+
+
+@pytest.mark.parametrize("n,n_tok,use_signs", [
+    (1024, 1, False), (5120, 1, False), (5120, 1, True), (17408, 1, True),
+    (5120, 3, True), (17408, 2, False), (32768, 1, False),
+    (1024, 4100, False), (2048, 2100, True)])      # the last two: one workgroup per token
+def test_rmsnorm_fwht_quant_bit_exact(n, n_tok, use_signs):
+    """Byte-exact against the host FWHT and quantiser applied to
+    (x * s) * w with the kernel's fp64-sum scale s."""
+    case(f"rmsnorm_fwht_quant n={n} n_tok={n_tok} signs={use_signs}")
+    X = (O.gen_normal(2100 + n + n_tok, n_tok * n) * 2.5).reshape(n_tok, n)
+    w = O.gen_normal(2101 + n, n) * 0.1 + 1
+    signs = (np.where(O.gen_normal(2102 + n, n) < 0, -1, 1)).astype(np.float32) if use_signs else None
+    eps = 1e-6
+    xq = torch.full((n // 32 * 36 * n_tok,), 0xAB, dtype=torch.uint8, device="cuda")
+    B.rmsnorm_fwht_quant(dev(X), dev(w), dev(signs) if use_signs else None, xq, n, n_tok, eps)
+    s = np.array([rms_scale_fp64(X[t], eps) for t in range(n_tok)], np.float32)
+    Y = ((X * s[:, None]).astype(np.float32) * w).astype(np.float32)
+    if use_signs:
+        Y = (Y * signs).astype(np.float32)
+    q = O.quantize_q8_1(O.fwht(Y.reshape(-1)), True)          # blocks are independent
+    exp = q.reshape(n_tok, n // 32, 36).transpose(1, 0, 2).reshape(-1)
+    np.testing.assert_array_equal(host(xq), exp)
+
+
+def test_rmsnorm_fwht_quant_against_reference_order():
+    """Against the reference's own chain (sequential fp32 sum of squares,
+    src/ops.h:13-22): the scales differ by that sum's rounding, so a few q
+    move by one step; d and every other byte agree."""
+    case("rmsnorm_fwht_quant vs sequential-sum chain, 4 x 17408")
+    n, n_tok, eps = 17408, 4, 1e-6
+    X = (O.gen_normal(2200, n_tok * n) * 1.5).reshape(n_tok, n)
+    w = O.gen_normal(2201, n) * 0.1 + 1
+    xq = torch.zeros(n // 32 * 36 * n_tok, dtype=torch.uint8, device="cuda")
+    B.rmsnorm_fwht_quant(dev(X), dev(w), None, xq, n, n_tok, eps)
+    ref = chunk_major([O.quantize_q8_1(O.fwht(O.rmsnorm(X[t], w, eps)), True) for t in range(n_tok)])
+    d_g, s_g, q_g = O.q81_fields(host(xq))
+    d_r, s_r, q_r = O.q81_fields(ref)
+    assert np.max(np.abs(d_g.astype(np.int32) - d_r.astype(np.int32))) <= 1        # fp16 ulps
+    dq = np.abs(q_g.astype(np.int32) - q_r.astype(np.int32))
+    assert dq.max() <= 1 and np.count_nonzero(dq) <= 1e-3 * dq.size
+    assert np.max(np.abs(s_g.astype(np.int32) - s_r.astype(np.int32))) <= 32
+
+
+def test_rmsnorm_fwht_quant_feeds_gemv():
+    """One token through the fused pre-pass then the GEMV equals the GEMV of
+    the emulated Q8_1 bit for bit."""
+    case("rmsnorm_fwht_quant -> gemv 6144x5120")
+    n_out, n = 6144, 5120
+    x = O.gen_normal(2300, n) * 3
+    w = O.gen_normal(2301, n) * 0.1 + 1
+    W = O.gen_weights(2302, n_out, n)
+    xq = torch.zeros(n // 32 * 36, dtype=torch.uint8, device="cuda")
+    B.rmsnorm_fwht_quant(dev(x), dev(w), None, xq, n, 1, 1e-6)
+    y = torch.zeros(n_out, dtype=torch.float32, device="cuda")
+    B.gemv(dev(W), xq, y, n_out, n)
+    s = rms_scale_fp64(x, 1e-6)
+    xq_e = O.quantize_q8_1(O.fwht(((x * s).astype(np.float32) * w).astype(np.float32)), True)
+    y2 = torch.zeros(n_out, dtype=torch.float32, device="cuda")
+    B.gemv(dev(W), dev(xq_e), y2, n_out, n)
+    np.testing.assert_array_equal(host(y).view(np.uint32), host(y2).view(np.uint32))
+
+
 # ----------------------------------------------------------------- rmsnorm
 def test_rmsnorm():
     case("rmsnorm 3x5120")

@@ -61,6 +61,10 @@ NULL = None
     ("bonsai_p40_fwht_gemv", (NULL, 16, NULL, NULL, 0, 1024), 0),     # empty no-op
     ("bonsai_p40_gemv_group", (NULL, NULL, NULL, 1, NULL, 128), 1),   # NULL arrays
     ("bonsai_p40_fwht_gemv_group", (NULL, NULL, NULL, 1, 16, NULL, 1024), 1),
+    ("bonsai_p40_rmsnorm_fwht_quant", (16, 16, NULL, 16, 1000, 1, C.c_float(1e-6)), 1),   # n % 1024
+    ("bonsai_p40_rmsnorm_fwht_quant", (16, NULL, NULL, 16, 1024, 1, C.c_float(1e-6)), 1),  # w NULL
+    ("bonsai_p40_rmsnorm_fwht_quant", (16, 16, NULL, 18, 1024, 1, C.c_float(1e-6)), 1),    # xq align
+    ("bonsai_p40_rmsnorm_fwht_quant", (16, 16, NULL, 16, 1024, 0, C.c_float(1e-6)), 0),    # no tokens
     ("bonsai_p40_rmsnorm", (NULL, NULL, NULL, 0, 64, C.c_float(1e-6)), 0),
     ("bonsai_p40_rmsnorm", (NULL, NULL, NULL, 4, 0, C.c_float(1e-6)), 1),
 ])

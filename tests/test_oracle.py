@@ -191,6 +191,30 @@ def test_swiglu_chain(golden):
     assert np.array_equal(O.quantize_q8_1(O.fwht(golden["f7_h"]), True), golden["f7_hq"])
 
 
+# ------------------------------------------------------------ RMSNorm (F8)
+@pytest.mark.parametrize("n", [3072, 1024])
+def test_rmsnorm_fixture(golden, n):
+    x, w, eps = golden[f"f8_{n}_x"], golden[f"f8_{n}_w"], float(golden[f"f8_{n}_eps"])
+    y = O.rmsnorm(x, w, eps)
+    np.testing.assert_array_equal(y.view(np.uint32), golden[f"f8_{n}_y"].view(np.uint32))
+    assert np.array_equal(O.quantize_q8_1(O.fwht(y), True), golden[f"f8_{n}_yq"])
+
+
+def test_rmsnorm_closed_form_and_planted_mistakes():
+    """Against the float64 formula; a missing eps, a sum over n-1 elements
+    or a mean taken as the plain sum must each fail the same check."""
+    n, eps = 4096, 1e-2
+    x = O.gen_normal(901, n) * 0.05                  # mean(x^2) ~ eps: eps matters
+    w = O.gen_normal(902, n) * 0.1 + 1
+    x64 = x.astype(np.float64)
+    exact = x64 / np.sqrt((x64 ** 2).mean() + eps) * w
+    tol = lambda y: np.max(np.abs(y - exact)) / np.max(np.abs(exact))   # noqa: E731
+    assert tol(O.rmsnorm(x, w, eps)) < 1e-5
+    assert tol(x64 / np.sqrt((x64 ** 2).mean()) * w) > 1e-3
+    assert tol(x64 / np.sqrt((x64[:-16] ** 2).sum() / n + eps) * w) > 1e-5
+    assert tol(x64 / np.sqrt((x64 ** 2).sum() + eps) * w) > 1e-3
+
+
 # ------------------------------------------------- planted-mistake checks
 def test_checks_detect_planted_mistakes(golden):
     """The fixture comparisons must fail for plausible oracle mistakes."""
