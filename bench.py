@@ -240,7 +240,10 @@ def bench_token_sweep(steps, warmup, gen, mode="separate"):
     separate pre-pass is faster.  "grouped": as a model runs it -- q/k/v and
     gate/up share their input, one grouped fused launch each
     (bonsai_p40_fwht_gemv_group), o fused, down with its pre-pass (4 GEMV
-    launches + 1 pre-pass per layer)."""
+    launches + 1 pre-pass per layer).  "layer": as "grouped", with both layer
+    inputs RMS-normalised inside the grouped launches
+    (bonsai_p40_rmsnorm_fwht_gemv_group) and the down projection fed by the
+    SwiGLU + FWHT + Q8_1 pre-pass of the gate/up outputs."""
     shapes = [(Q_DIM, N_EMBD), (KV_DIM, N_EMBD), (KV_DIM, N_EMBD), (N_EMBD, Q_DIM),
               (N_FF, N_EMBD), (N_FF, N_EMBD), (N_EMBD, N_FF)]
     proto = {s: synth_weights(s[0], s[1], gen) for s in set(shapes)}
@@ -252,8 +255,19 @@ def bench_token_sweep(steps, warmup, gen, mode="separate"):
 
     yk, yv, yg, yu = (torch.empty(n, device="cuda") for n in (KV_DIM, KV_DIM, N_FF, N_FF))
 
+    nw = torch.randn(N_EMBD, generator=gen, device="cuda") * 0.1 + 1
+
     def token(i):
         for L in layers:
+            if mode == "layer":
+                Wq, Wk, Wv, Wo, Wg, Wu, Wd = L
+                B.rmsnorm_fwht_gemv_group([Wq, Wk, Wv], xs[N_EMBD], nw, None, [ys[Q_DIM], yk, yv],
+                                          [Q_DIM, KV_DIM, KV_DIM], N_EMBD, 1e-6)
+                B.fwht_gemv(Wo, xs[Q_DIM], None, ys[N_EMBD], N_EMBD, Q_DIM)
+                B.rmsnorm_fwht_gemv_group([Wg, Wu], xs[N_EMBD], nw, None, [yg, yu], [N_FF, N_FF], N_EMBD, 1e-6)
+                B.swiglu_fwht_quant(yg, yu, None, qs[N_FF], N_FF)
+                B.gemv(Wd, qs[N_FF], ys[N_EMBD], N_EMBD, N_FF)
+                continue
             if mode == "grouped":
                 Wq, Wk, Wv, Wo, Wg, Wu, Wd = L
                 B.fwht_gemv_group([Wq, Wk, Wv], xs[N_EMBD], None, [ys[Q_DIM], yk, yv],
@@ -334,7 +348,7 @@ def main():
                     help="small-batch GEMM 17408x5120 with B tokens only (profiling)")
     ap.add_argument("--only-fused", action="store_true",
                     help="fused FWHT+Q8_1+GEMV 17408x5120 from fp32 only (profiling)")
-    ap.add_argument("--only-sweep", default="", metavar="MODE", choices=["", "separate", "fused", "grouped"],
+    ap.add_argument("--only-sweep", default="", metavar="MODE", choices=["", "separate", "fused", "grouped", "layer"],
                     help="config-2 token sweep in one mode only (profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:

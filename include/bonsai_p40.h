@@ -162,6 +162,20 @@ int bonsai_p40_gemv_group(const void * const * W, float * const * y, const int64
 int bonsai_p40_fwht_gemv_group(const void * const * W, float * const * y, const int64_t * n_out, int n_mat,
                                const float * x, const float * signs, int64_t n_in, bonsai_stream stream);
 
+// Layer-input grouped decode GEMV: y[m] = W[m] . Q8_1(FWHT(signs .* RMSNorm(x,
+// norm_w, eps))) for the n_mat (1..4) matrices that read one normalised layer
+// input (q/k/v after the attention norm, gate/up after the FFN norm), in one
+// launch in place of bonsai_p40_rmsnorm + bonsai_p40_fwht +
+// bonsai_p40_quant_activations + one bonsai_p40_gemv per matrix
+// (elementwise_p40.cu:48-88, 17-41 + gemv_p40.cu:168-219).  Every workgroup
+// normalises, rotates and quantises x into its own LDS; the sum of squares is
+// fp64 in a fixed order, so y[m] equals bonsai_p40_rmsnorm_fwht_quant followed
+// by bonsai_p40_gemv_group.  x and norm_w have n_in floats; signs may be NULL.
+// Errors: as bonsai_p40_fwht_gemv_group, plus 1 if norm_w is NULL.
+int bonsai_p40_rmsnorm_fwht_gemv_group(const void * const * W, float * const * y, const int64_t * n_out,
+                                       int n_mat, const float * x, const float * norm_w, const float * signs,
+                                       int64_t n_in, float eps, bonsai_stream stream);
+
 // Test hook: out[r * (n_in/32) + c] = the int32 chunk dot sum_k (code-1)*q of
 // row r, chunk c, computed by the same device code path as bonsai_p40_gemv
 // (the value of src/pq2_0.h:149-177 before scaling).  Errors as bonsai_p40_gemv.

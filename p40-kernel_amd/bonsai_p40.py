@@ -43,6 +43,7 @@ SIGNATURES = {
     "bonsai_p40_fwht_gemv": [_V, _F32P, _F32P, _F32P, _I64, _I64, _V],
     "bonsai_p40_gemv_group": [_V, _V, _V, C.c_int, _V, _I64, _V],
     "bonsai_p40_fwht_gemv_group": [_V, _V, _V, C.c_int, _F32P, _F32P, _I64, _V],
+    "bonsai_p40_rmsnorm_fwht_gemv_group": [_V, _V, _V, C.c_int, _F32P, _F32P, _F32P, _I64, C.c_float, _V],
     "bonsai_p40_chunk_dots": [_V, _V, _V, _I64, _I64, _V],
     "bonsai_p40_stream_read": [_V, _I64, _V, C.c_int, _V],
 }
@@ -180,6 +181,16 @@ def fwht_gemv_group(Ws, x, signs, ys, n_outs, n_in: int, stream=None) -> None:
     rc = lib().bonsai_p40_fwht_gemv_group(Wp, yp, np_, n, _ptr(x), _ptr(signs), n_in, _stream(stream))
     del keep
     _check("bonsai_p40_fwht_gemv_group", rc)
+
+
+def rmsnorm_fwht_gemv_group(Ws, x, norm_w, signs, ys, n_outs, n_in: int, eps: float,
+                            stream=None) -> None:
+    """y_m = W_m . Q8_1(FWHT(signs .* RMSNorm(x, norm_w, eps))), up to 4 matrices, one launch."""
+    keep, Wp, yp, np_, n = _group_arrays(Ws, ys, n_outs)
+    rc = lib().bonsai_p40_rmsnorm_fwht_gemv_group(Wp, yp, np_, n, _ptr(x), _ptr(norm_w), _ptr(signs), n_in,
+                                                  C.c_float(eps), _stream(stream))
+    del keep
+    _check("bonsai_p40_rmsnorm_fwht_gemv_group", rc)
 
 
 def chunk_dots(W, xq, out, n_out: int, n_in: int, stream=None) -> None:

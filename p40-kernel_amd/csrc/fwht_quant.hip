@@ -125,8 +125,7 @@ rms_rot_quant_kernel(const float * __restrict__ x, const float * __restrict__ w,
 #pragma unroll
         for (int r = 0; r < 16; ++r) ss += (double)v[r] * (double)v[r];
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    ss = wave_sum_f64(ss);
     if (l == 0) red[wave] = ss;
     __syncthreads();
     double tot = 0.0;
@@ -185,8 +184,7 @@ rms_rot_quant_block_kernel(const float * __restrict__ x, const float * __restric
     } else {
         for (int i = tid; i < n; i += 256) ss += (double)xt[i] * (double)xt[i];
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    ss = wave_sum_f64(ss);
     if (l == 0) red[wave] = ss;
     __syncthreads();
     if (wave != 0) return;

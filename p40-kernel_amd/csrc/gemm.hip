@@ -608,8 +608,9 @@ int launch_small_t(const uint8_t * W, const uint8_t * X, float * Y, int n_out, i
     auto kern = gemm_small_kernel<RT, KS, NT>;
     static bool attr = false;
     if (!attr) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS) != hipSuccess)
+            (void)hipGetLastError();   // a refused request must not linger as the launch's error
         attr = true;
     }
     hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(n_out, C::R)), dim3(64 * KS), C::LDS, st, W, X, Y,
@@ -649,8 +650,9 @@ int skinny_lds_limit() {
         if (hipDeviceGetAttribute(&x, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || x <= 0)
             x = 64 * 1024;
         v = x;
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_skinny_kernel),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, x);
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_skinny_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, x) != hipSuccess)
+            (void)hipGetLastError();   // a refused request must not linger as the launch's error
     }
     return v;
 }

@@ -246,6 +246,8 @@ struct MatGroup {
     float * y[MAX_GROUP];
     int n_out[MAX_GROUP];
     int u0[MAX_GROUP + 1];
+    const float * norm_w;       // RMSNorm weights of the fused rotation (RMS kernels only)
+    float eps;
 };
 
 MatGroup single_group(const void * W, float * y, int64_t n_out) {
@@ -313,6 +315,16 @@ __device__ __forceinline__ float * rot_sign_stage() {
     __shared__ __attribute__((aligned(16))) float buf[N];
     return buf;
 }
+template <int N>
+__device__ __forceinline__ float * rot_norm_stage() {
+    __shared__ __attribute__((aligned(16))) float buf[N];
+    return buf;
+}
+template <int N>
+__device__ __forceinline__ double * rms_partials() {
+    __shared__ double buf[N];
+    return buf;
+}
 
 // Workgroup of WAVES waves.  Each wave owns up to `units_per_wave` units
 // (grid-strided) and a private ring of D unit buffers in LDS; the workgroup shares one
@@ -340,7 +352,8 @@ __device__ __forceinline__ float * rot_sign_stage() {
 // unit p*nb + b = the 8 code bytes of chunk p of block b): the DMA moves the
 // same rows, only the lane's LDS offsets change (8-byte aligned code words,
 // no realignment).
-template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, bool GROUP = false, int NT = 1, bool RP = false>
+template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, bool GROUP = false, int NT = 1, bool RP = false,
+          bool RMS = false>
 __global__ void __launch_bounds__(64 * WAVES)
 gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * __restrict__ signs,
                int32_t * __restrict__ dump, int units_per_wave, int n_tok, int xcd_log2m) {
@@ -350,6 +363,7 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
     static_assert(D >= 1 && D <= 3, "ring depth");
     static_assert(D * P::NPL < 64, "vmcnt range");
     static_assert(ROT == 0 || P::NCH % 32 == 0, "the rotation needs whole 1024-element blocks");
+    static_assert(!RMS || ROT == 1 || ROT == 2, "RMSNorm rides on the fused rotation");
     constexpr int ACT_BYTES = Q81_BYTES * P::NCH * NT;
     constexpr int NA = (ACT_BYTES + 1023) / 1024;          // activation DMA instructions
     constexpr int NHB = P::NCH / 32;                       // Hadamard blocks of the row
@@ -412,6 +426,13 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
                     __builtin_amdgcn_global_load_lds(signs + HBLK * b + 256 * j + 4 * lane,
                                                      (lds_void *)(sst + HBLK * b + 256 * j), 16, 0, 0);
             }
+            if constexpr (RMS) {
+                float * nst = rot_norm_stage<NHB * HBLK>();
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    __builtin_amdgcn_global_load_lds(mg.norm_w + HBLK * b + 256 * j + 4 * lane,
+                                                     (lds_void *)(nst + HBLK * b + 256 * j), 16, 0, 0);
+            }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -468,11 +489,38 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         if (nu > 0) wait_vmcnt<D * P::NPL>();
         else wait_vmcnt<0>();
         const int row = fwht_row(lane);
+        // RMSNorm scale: each wave sums the squares of its own blocks in fp64
+        // (exact squares), the partials meet in LDS in wave order -- the same
+        // order in every workgroup, so all of them use the same scale
+        float rs = 1.0f;
+        if constexpr (RMS) {
+            double ss = 0.0;
+            for (int b = wave; b < NHB; b += WAVES) {
+                const float * xb = rot_x_stage<NHB * HBLK>() + HBLK * b + 16 * row;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) ss += (double)xb[r] * (double)xb[r];
+            }
+            ss = wave_sum_f64(ss);
+            double * part = rms_partials<WAVES>();
+            if (lane == 0) part[wave] = ss;
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            __builtin_amdgcn_s_barrier();
+            double tot = 0.0;
+#pragma unroll
+            for (int i = 0; i < WAVES; ++i) tot += part[i];
+            rs = 1.0f / sqrtf((float)(tot / (double)(NHB * HBLK)) + mg.eps);
+        }
         for (int b = wave; b < NHB; b += WAVES) {
             const float * xb = rot_x_stage<NHB * HBLK>() + HBLK * b + 16 * row;
             float v[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) v[r] = xb[r];
+            if constexpr (RMS) {
+#pragma clang fp contract(off)
+                const float * nb_ = rot_norm_stage<NHB * HBLK>() + HBLK * b + 16 * row;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) v[r] = v[r] * rs * nb_[r];
+            }
             if constexpr (ROT == 2) {
 #pragma clang fp contract(off)
                 const float * sb = rot_sign_stage<NHB * HBLK>() + HBLK * b + 16 * row;
@@ -680,8 +728,9 @@ int launch_stream_t(const uint8_t * W, const uint8_t * xq, float * y, int32_t * 
     auto kern = gemv_stream_kernel<G, NPL, DUMP>;
     static bool attr_set = false;
     if (!attr_set) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, max_lds_per_block());
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, max_lds_per_block()) != hipSuccess)
+            (void)hipGetLastError();   // a refused request must not linger as the launch's error
         attr_set = true;
     }
     const int n_units = (n_out + G - 1) / G;
@@ -735,13 +784,14 @@ int default_wg_per_cu(int nb, int64_t w_bytes) {
 }
 
 // LDS bytes of one gemv_nb_kernel workgroup (all static allocations)
-template <int NB, int D, int WAVES, int ROT, int NT = 1>
+template <int NB, int D, int WAVES, int ROT, int NT = 1, bool RMS = false>
 constexpr int nb_lds_bytes() {
     using P = NbSpec<NB, NT>;
     constexpr int act = (Q81_BYTES * P::NCH * NT + 1023) / 1024 * 1024;
     constexpr int ring = WAVES * (D + 1) * P::LDSB;
     constexpr int nhb = P::NCH / 32;
-    constexpr int stage = (ROT ? nhb * HBLK * 4 : 0) + (ROT == 2 ? nhb * HBLK * 4 : 0);   // ROT 3: x only
+    constexpr int stage = (ROT ? nhb * HBLK * 4 : 0) + (ROT == 2 ? nhb * HBLK * 4 : 0)   // ROT 3: x only
+                          + (RMS ? nhb * HBLK * 4 + 8 * WAVES : 0);
     return act + ring + stage;
 }
 
@@ -760,11 +810,11 @@ bool group_units(MatGroup & mg, int n_mat) {
     return u < 0x40000000;
 }
 
-template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, int NT = 1, bool RP = false>
+template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, int NT = 1, bool RP = false, bool RMS = false>
 int launch_nb_t(MatGroup mg, int n_mat, const void * xin, const float * signs, int32_t * dump,
                 int per_cu, hipStream_t st, int n_tok = 1) {
     using P = NbSpec<NB, NT>;
-    constexpr int lds = nb_lds_bytes<NB, D, WAVES, ROT, NT>();
+    constexpr int lds = nb_lds_bytes<NB, D, WAVES, ROT, NT, RMS>();
     static_assert(lds <= LDS_PER_CU, "workgroup LDS");
     if (!group_units<P::G>(mg, n_mat)) return 1;
     const int n_units = mg.u0[MAX_GROUP];
@@ -784,7 +834,14 @@ int launch_nb_t(MatGroup mg, int n_mat, const void * xin, const float * signs, i
     int xl = env_int("BONSAI_GEMV_XCD_LOG2M", 2);
     if (xl < 0 || xl > 3 || blocks % 8 != 0) xl = 0;
     while (xl > 0 && ((blocks / 8) * WAVES) % (1 << xl) != 0) --xl;
-    if constexpr (RP)
+    if constexpr (RMS) {
+        if (n_mat > 1)
+            hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, ROT, true, 1, false, true>), dim3(blocks),
+                               dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl);
+        else
+            hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, ROT, false, 1, false, true>), dim3(blocks),
+                               dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl);
+    } else if constexpr (RP)
         hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, ROT, false, 1, true>), dim3(blocks),
                            dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl);
     else if constexpr (NT > 1)
@@ -1059,18 +1116,18 @@ int launch_nb_small_nt(const uint8_t * W, const uint8_t * X, float * Y, int n_ou
 // at 6144x5120 and 5120x6144, against 9.9 / 7.0 / 6.8 us for the pre-pass
 // plus the GEMV; two workgroups per CU: 6.9 us at 5120x6144), else 4 waves
 // with D = 2 or D = 1.  Returns -1 when no shape fits the LDS of a workgroup.
-template <int NB, int ROT, bool RP = false>
+template <int NB, int ROT, bool RP = false, bool RMS = false>
 int launch_nb_rot(const MatGroup & mg, int n_mat, const float * x, const float * signs, hipStream_t st) {
     const int waves = env_int("BONSAI_FGEMV_WAVES", 8);
     int per_cu = env_int("BONSAI_GEMV_WG_PER_CU", 0);
     if (per_cu <= 0) per_cu = 1;
-    if constexpr (nb_lds_bytes<NB, 2, 8, ROT>() <= LDS_PER_CU) {
-        if (waves == 8) return launch_nb_t<NB, 2, 8, false, ROT, 1, RP>(mg, n_mat, x, signs, nullptr, per_cu, st);
+    if constexpr (nb_lds_bytes<NB, 2, 8, ROT, 1, RMS>() <= LDS_PER_CU) {
+        if (waves == 8) return launch_nb_t<NB, 2, 8, false, ROT, 1, RP, RMS>(mg, n_mat, x, signs, nullptr, per_cu, st);
     }
-    if constexpr (nb_lds_bytes<NB, 2, 4, ROT>() <= LDS_PER_CU)
-        return launch_nb_t<NB, 2, 4, false, ROT, 1, RP>(mg, n_mat, x, signs, nullptr, per_cu, st);
-    else if constexpr (nb_lds_bytes<NB, 1, 4, ROT>() <= LDS_PER_CU)
-        return launch_nb_t<NB, 1, 4, false, ROT, 1, RP>(mg, n_mat, x, signs, nullptr, per_cu, st);
+    if constexpr (nb_lds_bytes<NB, 2, 4, ROT, 1, RMS>() <= LDS_PER_CU)
+        return launch_nb_t<NB, 2, 4, false, ROT, 1, RP, RMS>(mg, n_mat, x, signs, nullptr, per_cu, st);
+    else if constexpr (nb_lds_bytes<NB, 1, 4, ROT, 1, RMS>() <= LDS_PER_CU)
+        return launch_nb_t<NB, 1, 4, false, ROT, 1, RP, RMS>(mg, n_mat, x, signs, nullptr, per_cu, st);
     else
         return -1;
 }
@@ -1078,20 +1135,41 @@ int launch_nb_rot(const MatGroup & mg, int n_mat, const float * x, const float *
 // Generic fused path (any n_in % 1024 == 0 whose Q8_1 activation fits in
 // LDS): every workgroup rotates and quantises the whole activation into LDS
 // (one Hadamard block per wave at a time), then each wave computes one row
-// with the lane-strided chunk walk of gemv_rowwave_kernel.
+// with the lane-strided chunk walk of gemv_rowwave_kernel.  With norm_w, x is
+// first RMS-normalised: the workgroup sums the squares of all of x in fp64 in
+// a fixed thread order (the same in every workgroup).
 __global__ void __launch_bounds__(GV_THREADS)
 gemv_rot_generic_kernel(const uint8_t * __restrict__ W, const float * __restrict__ x,
                         const float * __restrict__ signs, float * __restrict__ y, int n_out, int nb,
-                        bool vec) {
+                        bool vec, const float * __restrict__ norm_w, float eps) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ double red[GV_WAVES];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nchunk = 4 * nb;
     uint8_t * act = smem;
     const int xrow = fwht_row(lane);
+    float rs = 1.0f;
+    if (norm_w != nullptr) {
+        double ss = 0.0;
+        for (int i = threadIdx.x; i < 32 * nchunk; i += GV_THREADS) ss += (double)x[i] * (double)x[i];
+        ss = wave_sum_f64(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        double tot = 0.0;
+        for (int i = 0; i < GV_WAVES; ++i) tot += red[i];
+        rs = 1.0f / sqrtf((float)(tot / (double)(32 * nchunk)) + eps);
+    }
     for (int b = wave; b < nchunk / 32; b += GV_WAVES) {
         float v[16];
         load16(x + (size_t)HBLK * b + 16 * xrow, v, vec);
+        if (norm_w != nullptr) {
+#pragma clang fp contract(off)
+            float wv[16];
+            load16(norm_w + (size_t)HBLK * b + 16 * xrow, wv, vec);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) v[r] = v[r] * rs * wv[r];
+        }
         if (signs != nullptr) {
 #pragma clang fp contract(off)
             float sg[16];
@@ -1136,34 +1214,54 @@ bool group_w_aligned(const MatGroup & mg, int n_mat) {
 // widths, else one generic fused launch per matrix.
 int fwht_gemv_group_dispatch(const MatGroup & mg, int n_mat, const float * x, const float * signs,
                              int64_t n_in, hipStream_t st) {
-    const bool al = group_w_aligned(mg, n_mat) && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)signs & 15u) == 0;
+    const bool al = group_w_aligned(mg, n_mat) && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)signs & 15u) == 0 &&
+                    ((uintptr_t)mg.norm_w & 15u) == 0;
     if (al && env_int("BONSAI_GEMV_KERNEL", 0) == 0) {
         int rc = -1;
+        if (mg.norm_w != nullptr) {
+            // RMSNorm on the widths a layer input has (the model's 5120 and 6144,
+            // and 1024); other widths take the generic kernel below
+#define PQ2_RMS_CASE(N)                                                                         \
+    case N: rc = signs ? launch_nb_rot<N, 2, false, true>(mg, n_mat, x, signs, st)              \
+                       : launch_nb_rot<N, 1, false, true>(mg, n_mat, x, signs, st); break;
+            switch (n_in / QK_PQ2) {
+                PQ2_RMS_CASE(8) PQ2_RMS_CASE(40) PQ2_RMS_CASE(48)
+                default: break;
+            }
+#undef PQ2_RMS_CASE
+        } else {
 #define PQ2_ROT_CASE(N)                                                                         \
     case N: rc = signs ? launch_nb_rot<N, 2>(mg, n_mat, x, signs, st)                           \
                        : launch_nb_rot<N, 1>(mg, n_mat, x, signs, st); break;
-        switch (n_in / QK_PQ2) {
-            PQ2_ROT_CASE(8) PQ2_ROT_CASE(40) PQ2_ROT_CASE(48) PQ2_ROT_CASE(80) PQ2_ROT_CASE(96)
-            PQ2_ROT_CASE(136)
-            default: break;
-        }
+            switch (n_in / QK_PQ2) {
+                PQ2_ROT_CASE(8) PQ2_ROT_CASE(40) PQ2_ROT_CASE(48) PQ2_ROT_CASE(80) PQ2_ROT_CASE(96)
+                PQ2_ROT_CASE(136)
+                default: break;
+            }
 #undef PQ2_ROT_CASE
+        }
         if (rc >= 0) return rc;
     }
     const size_t lds = rot_generic_lds(n_in);
     if (lds > (size_t)max_lds_per_block()) return 1;
     static bool attr_set = false;
     if (!attr_set) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_rot_generic_kernel),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, max_lds_per_block());
+        // the kernel's static LDS (its fp64 partial sums) comes off the maximum;
+        // a refused request must not linger as the launch's error
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_rot_generic_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                max_lds_per_block() - 1024) != hipSuccess)
+            (void)hipGetLastError();
         attr_set = true;
     }
-    const bool vec = ((uintptr_t)x & 15u) == 0 && ((uintptr_t)signs & 15u) == 0;
+    if (lds > (size_t)max_lds_per_block() - 1024) return 1;
+    const bool vec = ((uintptr_t)x & 15u) == 0 && ((uintptr_t)signs & 15u) == 0 &&
+                     ((uintptr_t)mg.norm_w & 15u) == 0;
     for (int m = 0; m < n_mat; ++m) {
         if (mg.n_out[m] <= 0) continue;
         const unsigned blocks = (unsigned)((mg.n_out[m] + GV_WAVES - 1) / GV_WAVES);
         hipLaunchKernelGGL(gemv_rot_generic_kernel, dim3(blocks), dim3(GV_THREADS), lds, st, mg.W[m], x,
-                           signs, mg.y[m], mg.n_out[m], (int)(n_in / QK_PQ2), vec);
+                           signs, mg.y[m], mg.n_out[m], (int)(n_in / QK_PQ2), vec, mg.norm_w, mg.eps);
         const int rc = (int)hipGetLastError();
         if (rc != 0) return rc;
     }
@@ -1312,7 +1410,7 @@ int bonsai_p40_gemv_group(const void * const * W, float * const * y, const int64
                           const void * xq, int64_t n_in, bonsai_stream stream) {
     if (n_in <= 0 || n_in % QK_PQ2 != 0 || ((uintptr_t)xq & 3u) != 0) return 1;
     if (n_in / QK_PQ2 > (1 << 24)) return 1;
-    MatGroup mg;
+    MatGroup mg{};
     int64_t rows = 0;
     if (make_group(mg, W, y, n_out, n_mat, &rows) != 0) return 1;
     if (rows == 0) return 0;
@@ -1331,10 +1429,24 @@ int bonsai_p40_fwht_gemv_group(const void * const * W, float * const * y, const 
                                const float * x, const float * signs, int64_t n_in, bonsai_stream stream) {
     if (n_in <= 0 || n_in % HBLK != 0 || x == nullptr) return 1;
     if (n_in / QK_PQ2 > (1 << 24)) return 1;
-    MatGroup mg;
+    MatGroup mg{};
     int64_t rows = 0;
     if (make_group(mg, W, y, n_out, n_mat, &rows) != 0) return 1;
     if (rows == 0) return 0;
+    return fwht_gemv_group_dispatch(mg, n_mat, x, signs, n_in, (hipStream_t)stream);
+}
+
+int bonsai_p40_rmsnorm_fwht_gemv_group(const void * const * W, float * const * y, const int64_t * n_out,
+                                       int n_mat, const float * x, const float * norm_w, const float * signs,
+                                       int64_t n_in, float eps, bonsai_stream stream) {
+    if (n_in <= 0 || n_in % HBLK != 0 || x == nullptr || norm_w == nullptr) return 1;
+    if (n_in / QK_PQ2 > (1 << 24)) return 1;
+    MatGroup mg{};
+    int64_t rows = 0;
+    if (make_group(mg, W, y, n_out, n_mat, &rows) != 0) return 1;
+    if (rows == 0) return 0;
+    mg.norm_w = norm_w;
+    mg.eps = eps;
     return fwht_gemv_group_dispatch(mg, n_mat, x, signs, n_in, (hipStream_t)stream);
 }
 

@@ -81,6 +81,33 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v) {
     return v;
 }
 
+// fp64 moves and sum over the 64 lanes of a wave, the total in every lane:
+// rows of 16 by quad/mirror DPP moves of both halves, then the four row sums
+// (read from lanes 0, 16, 32, 48) added in a fixed order.  No LDS round trips
+// (a __shfl_xor of a double is two ds_bpermute per step).
+template <int CTRL>
+__device__ __forceinline__ double dpp_mov_f64(double v) {
+    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xf, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xf, 0xf, false);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    v += dpp_mov_f64<DPP_QUAD_XOR1>(v);
+    v += dpp_mov_f64<DPP_QUAD_XOR2>(v);
+    v += dpp_mov_f64<DPP_ROW_HALF_MIRROR>(v);
+    v += dpp_mov_f64<DPP_ROW_MIRROR>(v);
+    return (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
+}
+
 // ---- integer chunk dot ------------------------------------------------------
 // sumi = bias + sum_k dot4((w >> 2k) & 0x03030303, a_k) over the two 16-code
 // words (w0, w1) of a 32-weight chunk against the 8 permuted activation words

@@ -183,8 +183,9 @@ int bonsai_p40_gemv_repack(const void * W, const float * x, float * y, int64_t n
     if (lds > (size_t)lds_limit()) return 1;
     static bool attr_set = false;
     if (!attr_set) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_repack_kernel),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds_limit());
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_repack_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds_limit()) != hipSuccess)
+            (void)hipGetLastError();   // a refused request must not linger as the launch's error
         attr_set = true;
     }
     int64_t blocks = (n_out + RP_WAVES - 1) / RP_WAVES;

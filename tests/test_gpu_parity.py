@@ -311,6 +311,67 @@ def test_fwht_gemv_group(n_in, n_outs, signed):
         np.testing.assert_array_equal(bits(got), bits(host(y1)))
 
 
+RMS_GROUPS = [
+    (5120, (6144, 1024, 1024), True),         # q, k, v after the attention norm
+    (5120, (17408, 17408), False),            # gate, up after the FFN norm
+    (5120, (17407, 3, 0, 1001), True),        # ragged
+    (6144, (5120, 7), False),
+    (1024, (300, 64), True),
+    (2048, (64, 300), True),                  # no streaming kernel: generic fused kernel
+    (17408, (100, 33), False),                # no RMS streaming instance: generic fused kernel
+]
+
+
+@pytest.mark.parametrize("n_in,n_outs,signed", RMS_GROUPS)
+def test_rmsnorm_fwht_gemv_group(n_in, n_outs, signed):
+    """Bit-identical to the fused RMSNorm pre-pass followed by the grouped
+    GEMV (both scale with an fp64 sum of squares), and within the fp32
+    tolerance of the oracle chain with that scale."""
+    case(f"rmsnorm_fwht_gemv_group n_in={n_in} n_outs={n_outs} signed={signed}")
+    Ws = [O.gen_weights(2400 + m + n_in, max(r, 1), n_in) for m, r in enumerate(n_outs)]
+    x = O.gen_normal(2410 + n_in, n_in) * 4
+    nw = O.gen_normal(2411 + n_in, n_in) * 0.1 + 1
+    s = np.where(O.gen_normal(2412 + n_in, n_in) > 0, 1.0, -1.0).astype(np.float32) if signed else None
+    eps = 1e-6
+    Wd = [dev(W) for W in Ws]
+    xd, nwd = dev(x), dev(nw)
+    sd = None if s is None else dev(s)
+    ys = [torch.full((max(r, 1),), float("nan"), dtype=torch.float32, device="cuda") for r in n_outs]
+    B.rmsnorm_fwht_gemv_group(Wd, xd, nwd, sd, ys, n_outs, n_in, eps)
+    xq = torch.zeros(n_in // 32 * 36, dtype=torch.uint8, device="cuda")
+    B.rmsnorm_fwht_quant(xd, nwd, sd, xq, n_in, 1, eps)
+    rs = rms_scale_fp64(x, eps)
+    xq_o = O.quantize_q8_1(O.fwht(((x * rs).astype(np.float32) * nw).astype(np.float32), s), True)
+    np.testing.assert_array_equal(host(xq), xq_o)
+    for W, Wdm, y, r in zip(Ws, Wd, ys, n_outs):
+        got = host(y)
+        if r == 0:
+            assert np.isnan(got).all()
+            continue
+        assert normwise(got, O.gemv(W, xq_o, r, n_in, nthreads=16)) <= TOL
+        y1 = torch.full((r,), float("nan"), dtype=torch.float32, device="cuda")
+        B.gemv(Wdm, xq, y1, r, n_in)
+        np.testing.assert_array_equal(bits(got), bits(host(y1)))
+
+
+def test_rmsnorm_fwht_gemv_group_unaligned_x():
+    """x 4 bytes past a 16-byte boundary: the generic fused kernel (its own
+    fp32 summation order), within the tolerance of the oracle GEMV on the
+    same Q8_1 activation."""
+    case("rmsnorm_fwht_gemv_group unaligned x 5120")
+    n_in, r = 5120, 500
+    W = O.gen_weights(2500, r, n_in)
+    x = O.gen_normal(2501, n_in + 1)
+    nw = O.gen_normal(2502, n_in) * 0.1 + 1
+    xbuf = dev(x)
+    xv = xbuf[1:]
+    y = torch.full((r,), float("nan"), dtype=torch.float32, device="cuda")
+    B.rmsnorm_fwht_gemv_group([dev(W)], xv, dev(nw), None, [y], [r], n_in, 1e-6)
+    rs = rms_scale_fp64(x[1:], 1e-6)
+    xq_o = O.quantize_q8_1(O.fwht(((x[1:] * rs).astype(np.float32) * nw).astype(np.float32)), True)
+    assert normwise(host(y), O.gemv(W, xq_o, r, n_in, nthreads=16)) <= TOL
+
+
 @pytest.mark.parametrize("x_offset", [4, 8])
 def test_fwht_gemv_unaligned_x(x_offset):
     case(f"fwht_gemv unaligned x offset {x_offset}")

@@ -85,6 +85,9 @@ def test_group_argument_checks():
     assert L.bonsai_p40_gemv_group(Wp, yp, np_, 3, None, 100, None) == 1         # n_in % 128
     assert L.bonsai_p40_fwht_gemv_group(Wp, yp, np_, 2, 16, None, 1024, None) == 0
     assert L.bonsai_p40_fwht_gemv_group(Wp, yp, np_, 2, 16, None, 2000, None) == 1
+    assert L.bonsai_p40_rmsnorm_fwht_gemv_group(Wp, yp, np_, 2, 16, 16, None, 1024, C.c_float(1e-6), None) == 0
+    assert L.bonsai_p40_rmsnorm_fwht_gemv_group(Wp, yp, np_, 2, 16, None, None, 1024, C.c_float(1e-6), None) == 1
+    assert L.bonsai_p40_rmsnorm_fwht_gemv_group(Wp, yp, np_, 2, 16, 16, None, 1000, C.c_float(1e-6), None) == 1
     n[1] = 1 << 30
     assert L.bonsai_p40_gemv_group(Wp, yp, np_, 2, None, 128, None) == 1         # too many rows
 
