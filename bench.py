@@ -457,7 +457,9 @@ def main():
         print(f"[bench] token sweep: {extra['token_sweep_config2']}", file=sys.stderr, flush=True)
         for mode, note in (("fused", "FWHT+Q8_1 inside each GEMV launch (down: separate pre-pass)"),
                            ("grouped", "q/k/v and gate/up as grouped fused launches, o fused, "
-                                       "down with its pre-pass: 4 GEMV launches + 1 pre-pass per layer")):
+                                       "down with its pre-pass: 4 GEMV launches + 1 pre-pass per layer"),
+                           ("layer", "as grouped, with both layer RMSNorms inside the grouped launches "
+                                     "and SwiGLU+FWHT+Q8_1 of the gate/up outputs feeding down")):
             m, wb = bench_token_sweep(5, 2, gen, mode=mode)
             extra[f"token_sweep_config2_{mode}"] = {"ms_per_token": round(m, 3), "tok/s": round(1e3 / m, 2),
                                                     "weight_GB/s": round(wb / (m * 1e-3) / 1e9, 1),

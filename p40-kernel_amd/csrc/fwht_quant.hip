@@ -1,9 +1,9 @@
 // fwht_quant.hip -- activation pre-pass kernels for gfx950:
 //   * FWHT-1024 (normalised Sylvester-Hadamard, optional +-1 signs),
 //   * permuted Q8_1 quantisation with the reference host rounding,
-//   * both fused into one LDS-resident butterfly kernel, optionally preceded
-//     by SwiGLU (the FFN glue) and writing the GEMV (token-major) or the GEMM
-//     (chunk-major) activation layout;
+//   * both fused into one register-resident butterfly kernel, writing the
+//     GEMV (token-major) or the GEMM (chunk-major) activation layout;
+//   * SwiGLU (the FFN glue) -> FWHT -> Q8_1, the SwiGLU spread over 4 waves;
 //   * RMSNorm -> FWHT -> Q8_1 of token rows in one launch (the step before
 //     every projection of a layer).
 //
@@ -32,7 +32,6 @@ namespace {
 enum : int {
     M_ROT = 1,        // apply the FWHT
     M_SIGNS = 2,      // multiply by signs first
-    M_SWIGLU = 4,     // input = silu(gate) * up
     M_OUT_F32 = 8,    // write the rotated fp32 block back
     M_OUT_Q8 = 16,    // write permuted Q8_1
     M_CHUNK_MAJOR = 32,
@@ -41,11 +40,10 @@ enum : int {
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
-// Grid (n/1024, n_tok), 64 threads.  `x` (and `up` for SwiGLU) are [n_tok][n].
+// Grid (n/1024, n_tok), 64 threads.  `x` is [n_tok][n].
 template <int MODE>
 __global__ void __launch_bounds__(64)
-rot_quant_kernel(const float * __restrict__ x, const float * __restrict__ up,
-                 const float * __restrict__ signs, float * __restrict__ xout,
+rot_quant_kernel(const float * __restrict__ x, const float * __restrict__ signs, float * __restrict__ xout,
                  uint8_t * __restrict__ q, int n, int n_tok) {
     const int l = threadIdx.x;
     const int blk = blockIdx.x;
@@ -56,12 +54,6 @@ rot_quant_kernel(const float * __restrict__ x, const float * __restrict__ up,
 
     float v[16];
     load16(x + base, v, vec);
-    if (MODE & M_SWIGLU) {
-        float u[16];
-        load16(up + base, u, vec);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = silu(v[r]) * u[r];
-    }
     if (MODE & M_SIGNS) {
         float sg[16];
         load16(signs + (size_t)blk * HBLK + 16 * row, sg, vec);
@@ -201,17 +193,61 @@ rms_rot_quant_block_kernel(const float * __restrict__ x, const float * __restric
     quant_pair_store(v, q + (c * n_tok + tok) * Q81_BYTES, row & 1);
 }
 
+// SwiGLU -> FWHT -> Q8_1 of one token, 4 waves per Hadamard block: the
+// SwiGLU (an expf and an IEEE division per element, the bulk of the work) is
+// spread over all 256 threads, 4 elements each, into LDS; wave 0 then loads
+// the block in the FWHT lane layout, applies the signs, rotates and
+// quantises.  Element values are those of the one-wave kernel (same silu()).
+template <bool VEC, bool SIGNS>
+__global__ void __launch_bounds__(256)
+swiglu_rot_quant_kernel(const float * __restrict__ gate, const float * __restrict__ up,
+                        const float * __restrict__ signs, uint8_t * __restrict__ q) {
+    __shared__ __attribute__((aligned(16))) float h[HBLK];
+    const int tid = threadIdx.x, l = tid & 63;
+    const size_t base = (size_t)blockIdx.x * HBLK;
+    float g[4], u[4];
+    if constexpr (VEC) {
+        const float4 g4 = reinterpret_cast<const float4 *>(gate + base)[tid];
+        const float4 u4 = reinterpret_cast<const float4 *>(up + base)[tid];
+        g[0] = g4.x; g[1] = g4.y; g[2] = g4.z; g[3] = g4.w;
+        u[0] = u4.x; u[1] = u4.y; u[2] = u4.z; u[3] = u4.w;
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) { g[k] = gate[base + 4 * tid + k]; u[k] = up[base + 4 * tid + k]; }
+    }
+    float4 r;
+    r.x = silu(g[0]) * u[0]; r.y = silu(g[1]) * u[1]; r.z = silu(g[2]) * u[2]; r.w = silu(g[3]) * u[3];
+    reinterpret_cast<float4 *>(h)[tid] = r;
+    __syncthreads();
+    if (tid >= 64) return;
+    const int row = fwht_row(l);
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float4 t = reinterpret_cast<const float4 *>(h + 16 * row)[k];
+        v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w;
+    }
+    if constexpr (SIGNS) {
+        float sg[16];
+        load16(signs + base + 16 * row, sg, VEC);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] *= sg[k];
+    }
+    fwht1024_regs(v, l);
+    quant_pair_store(v, q + ((size_t)blockIdx.x * (HBLK / QK8) + (row >> 1)) * Q81_BYTES, row & 1);
+}
+
 inline bool al16(const void * p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 inline bool al4(const void * p) { return ((uintptr_t)p & 3u) == 0; }
 
 template <int MODE>
-int launch_rot(const float * x, const float * up, const float * signs, float * xout, void * q,
+int launch_rot(const float * x, const float * signs, float * xout, void * q,
                int64_t n, int64_t n_tok, hipStream_t st) {
     dim3 grid((unsigned)(n / HBLK), (unsigned)n_tok);
-    const bool vec = al16(x) && al16(up) && al16(signs) && al16(xout);
+    const bool vec = al16(x) && al16(signs) && al16(xout);
     const bool sg = signs != nullptr;
 #define PQ2_ROT_LAUNCH(M)                                                                         \
-    hipLaunchKernelGGL(rot_quant_kernel<(M)>, grid, dim3(64), 0, st, x, up, signs, xout,         \
+    hipLaunchKernelGGL(rot_quant_kernel<(M)>, grid, dim3(64), 0, st, x, signs, xout,         \
                        (uint8_t *)q, (int)n, (int)n_tok)
     if (vec && sg) PQ2_ROT_LAUNCH(MODE | M_VEC | M_SIGNS);
     else if (vec) PQ2_ROT_LAUNCH(MODE | M_VEC);
@@ -244,7 +280,7 @@ extern "C" {
 int bonsai_p40_fwht(float * x, const float * signs, int64_t n, bonsai_stream stream) {
     if (n <= 0 || n % HBLK != 0 || x == nullptr) return 1;
     if (n / HBLK > 0x7fffffff) return 1;
-    return launch_rot<M_ROT | M_OUT_F32>(x, nullptr, signs, x, nullptr, n, 1, (hipStream_t)stream);
+    return launch_rot<M_ROT | M_OUT_F32>(x, signs, x, nullptr, n, 1, (hipStream_t)stream);
 }
 
 int bonsai_p40_quant_activations(const float * x, void * out, int64_t n, bonsai_stream stream) {
@@ -256,7 +292,7 @@ int bonsai_p40_quant_activations(const float * x, void * out, int64_t n, bonsai_
 int bonsai_p40_fwht_quant(const float * x, const float * signs, void * xq, int64_t n,
                           bonsai_stream stream) {
     if (n <= 0 || n % HBLK != 0 || !al4(xq)) return 1;
-    return launch_rot<M_ROT | M_OUT_Q8>(x, nullptr, signs, nullptr, xq, n, 1, (hipStream_t)stream);
+    return launch_rot<M_ROT | M_OUT_Q8>(x, signs, nullptr, xq, n, 1, (hipStream_t)stream);
 }
 
 int bonsai_p40_quant_tokens(const float * X, const float * signs, void * Xq, int64_t n,
@@ -265,7 +301,7 @@ int bonsai_p40_quant_tokens(const float * X, const float * signs, void * Xq, int
     if (n % (rotate ? HBLK : QK8) != 0) return 1;
     if (n * n_tok > ((int64_t)1 << 40)) return 1;
     if (rotate)
-        return launch_rot<M_ROT | M_OUT_Q8 | M_CHUNK_MAJOR>(X, nullptr, signs, nullptr, Xq, n, n_tok,
+        return launch_rot<M_ROT | M_OUT_Q8 | M_CHUNK_MAJOR>(X, signs, nullptr, Xq, n, n_tok,
                                                             (hipStream_t)stream);
     if (signs != nullptr) return 1;   // signs only apply with the rotation
     return launch_quant(X, Xq, n, n_tok, true, (hipStream_t)stream);
@@ -300,8 +336,15 @@ int bonsai_p40_rmsnorm_fwht_quant(const float * x, const float * w, const float 
 int bonsai_p40_swiglu_fwht_quant(const float * gate, const float * up, const float * signs,
                                  void * xq, int64_t n, bonsai_stream stream) {
     if (n <= 0 || n % HBLK != 0 || !al4(xq)) return 1;
-    return launch_rot<M_ROT | M_OUT_Q8 | M_SWIGLU>(gate, up, signs, nullptr, xq, n, 1,
-                                                   (hipStream_t)stream);
+    if (n / HBLK > 0x7fffffff) return 1;
+    const bool vec = al16(gate) && al16(up) && al16(signs);
+    const dim3 grid((unsigned)(n / HBLK));
+    hipStream_t st = (hipStream_t)stream;
+    if (vec && signs) hipLaunchKernelGGL((swiglu_rot_quant_kernel<true, true>), grid, dim3(256), 0, st, gate, up, signs, (uint8_t *)xq);
+    else if (vec) hipLaunchKernelGGL((swiglu_rot_quant_kernel<true, false>), grid, dim3(256), 0, st, gate, up, signs, (uint8_t *)xq);
+    else if (signs) hipLaunchKernelGGL((swiglu_rot_quant_kernel<false, true>), grid, dim3(256), 0, st, gate, up, signs, (uint8_t *)xq);
+    else hipLaunchKernelGGL((swiglu_rot_quant_kernel<false, false>), grid, dim3(256), 0, st, gate, up, signs, (uint8_t *)xq);
+    return (int)hipGetLastError();
 }
 
 }  // extern "C"

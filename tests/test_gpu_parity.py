@@ -137,6 +137,27 @@ def test_swiglu_fwht_quant_fixture(golden):
     assert np.max(np.abs(d1.astype(int) - d2.astype(int))) <= 1
 
 
+@pytest.mark.parametrize("n,signed,offset", [(17408, True, 0), (5120, False, 1), (1024, True, 0)])
+def test_swiglu_fwht_quant_seeded(n, signed, offset):
+    """Against the oracle chain (glibc expf): q within one step, rare."""
+    case(f"swiglu_fwht_quant n={n} signed={signed} float offset={offset}")
+    g = O.gen_normal(2600 + n, n) * 2
+    u = O.gen_normal(2601 + n, n)
+    sg = np.where(O.gen_normal(2602 + n, n) > 0, 1.0, -1.0).astype(np.float32) if signed else None
+    gb = torch.zeros(n + 4, dtype=torch.float32, device="cuda")
+    ub = torch.zeros(n + 4, dtype=torch.float32, device="cuda")
+    gb[offset:offset + n] = dev(g)
+    ub[offset:offset + n] = dev(u)
+    q = torch.zeros(n // 32 * 36, dtype=torch.uint8, device="cuda")
+    B.swiglu_fwht_quant(gb.data_ptr() + 4 * offset, ub.data_ptr() + 4 * offset,
+                        None if sg is None else dev(sg), q, n)
+    d1, s1, q1 = O.q81_fields(host(q))
+    d2, s2, q2 = O.q81_fields(O.quantize_q8_1(O.fwht(O.swiglu(g, u), sg), True))
+    assert np.max(np.abs(q1.astype(int) - q2.astype(int))) <= 1
+    assert np.mean(q1 != q2) < 0.01
+    assert np.max(np.abs(d1.astype(int) - d2.astype(int))) <= 1
+
+
 # --------------------------------------------------------- chunk dots / GEMV
 SHAPES = [
     (8, 5120), (5, 5120), (1, 5120), (64, 17408), (33, 6144), (7, 1024), (9, 10240),
