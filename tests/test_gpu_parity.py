@@ -498,10 +498,11 @@ def test_gemm_prefill_shapes_row_sample(n_out, n_in, n_tok):
 @pytest.mark.parametrize("n_out,n_in,n_tok", [
     (17408, 5120, 2), (6144, 5120, 3), (1025, 5120, 4), (5120, 6144, 2), (77, 6144, 4),
     (333, 1024, 3), (64, 10240, 2), (31, 12288, 2), (17407, 5120, 2), (5120, 17408, 2),
-    (301, 17408, 3), (100, 17408, 4), (257, 12288, 4)])
+    (301, 17408, 3), (100, 17408, 4), (257, 12288, 4), (5120, 17408, 4)])
 def test_gemm_small_batch_streaming(n_out, n_in, n_tok):
     """2 tokens run on the streaming GEMV kernel with per-token planes (3 on
-    the widths without a 4x4x4 kernel), 3..4 on the 4x4x4 MFMA kernel:
+    the widths without a 4x4x4 kernel), 3..4 on the 4x4x4 MFMA kernel (4 on
+    the other widths on the 16x16 MFMA kernel):
     against the oracle, and against one GEMV per token (bit-identical for 2
     tokens, where the unit shape and the arithmetic are the GEMV's)."""
     case(f"gemm small batch {n_out}x{n_in}x{n_tok}")
