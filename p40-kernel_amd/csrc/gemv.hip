@@ -353,7 +353,7 @@ __device__ __forceinline__ double * rms_partials() {
 // same rows, only the lane's LDS offsets change (8-byte aligned code words,
 // no realignment).
 template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, bool GROUP = false, int NT = 1, bool RP = false,
-          bool RMS = false>
+          bool RMS = false, bool OVL = false>
 __global__ void __launch_bounds__(64 * WAVES)
 gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * __restrict__ signs,
                int32_t * __restrict__ dump, int units_per_wave, int n_tok, int xcd_log2m) {
@@ -364,6 +364,7 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
     static_assert(D * P::NPL < 64, "vmcnt range");
     static_assert(ROT == 0 || P::NCH % 32 == 0, "the rotation needs whole 1024-element blocks");
     static_assert(!RMS || ROT == 1 || ROT == 2, "RMSNorm rides on the fused rotation");
+    static_assert(!OVL || (ROT == 1 && !RMS && !RP && NT == 1), "ring-staged rotation: plain FWHT");
     constexpr int ACT_BYTES = Q81_BYTES * P::NCH * NT;
     constexpr int NA = (ACT_BYTES + 1023) / 1024;          // activation DMA instructions
     constexpr int NHB = P::NCH / 32;                       // Hadamard blocks of the row
@@ -400,6 +401,12 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
     const int NW = gridDim.x * WAVES;
     const int nu = gw < n_units ? min(units_per_wave, (n_units - 1 - gw) / NW + 1) : 0;
 
+    // OVL: the fp32 blocks are staged in the unit ring itself (the widest rows,
+    // where a separate stage does not fit beside an 8-wave ring): slots k =
+    // 0..NBW-1 of a wave hold blocks min(wave + WAVES k, NHB - 1) in registers
+    constexpr int NBW = OVL ? (NHB + WAVES - 1) / WAVES : 1;
+    float xr[NBW][16];
+
     // 1. activation: ROT = 0 -- this wave's share of the Q8_1 DMA
     //    (instructions k = wave, wave + WAVES, ...); ROT > 0 -- the fp32
     //    blocks (and signs) of this wave into its staging areas
@@ -411,6 +418,29 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
             const int off = min(16 * (64 * k + lane), act_bytes - 16);
             __builtin_amdgcn_global_load_lds(xq + off, (lds_void *)(&act_lds[1024 * k]), 16, 0, 0);
         }
+    } else if constexpr (OVL) {
+        // the blocks go through the ring before any unit: DMA, wait for all of
+        // it (nothing else is in flight), copy the wave's blocks into
+        // registers, and release the ring with a workgroup barrier
+        static_assert(NHB * HBLK * 4 <= WAVES * SL * P::LDSB, "the staged blocks fit in the ring");
+        const float * x = static_cast<const float *>(xin);
+        float * xst = reinterpret_cast<float *>(&ring_all[0][0][0]);
+        for (int b = wave; b < NHB; b += WAVES) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                __builtin_amdgcn_global_load_lds(x + HBLK * b + 256 * j + 4 * lane,
+                                                 (lds_void *)(xst + HBLK * b + 256 * j), 16, 0, 0);
+        }
+        wait_vmcnt<0>();
+        const int xrow = fwht_row(lane);
+#pragma unroll
+        for (int k = 0; k < NBW; ++k) {
+            const float * xb = xst + HBLK * min(wave + WAVES * k, NHB - 1) + 16 * xrow;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) xr[k][r] = xb[r];
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);        // lgkmcnt(0): the wave's reads are done
+        __builtin_amdgcn_s_barrier();
     } else {
         const float * x = static_cast<const float *>(xin);
         float * xst = rot_x_stage<NHB * HBLK>();
@@ -480,6 +510,22 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         //    workgroup barrier makes every share visible
         if (nu > 0) wait_vmcnt<D * P::NPL>();
         else wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        if (nu <= 0) return;
+    } else if constexpr (OVL) {
+        // 3. rotate and quantise the register blocks (a repeated one is rotated
+        //    and not stored) while the first units stream in, then the barrier
+        const int xrow = fwht_row(lane);
+#pragma unroll
+        for (int k = 0; k < NBW; ++k) {
+            const int b = wave + WAVES * k;
+            float v[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) v[r] = xr[k][r];
+            fwht1024_regs(v, lane);
+            if (b < NHB) quant_pair_store(v, &act_lds[Q81_BYTES * (32 * b + (xrow >> 1))], xrow & 1);
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);        // lgkmcnt(0): this wave's LDS stores are done
         __builtin_amdgcn_s_barrier();
         if (nu <= 0) return;
     } else {
@@ -784,13 +830,13 @@ int default_wg_per_cu(int nb, int64_t w_bytes) {
 }
 
 // LDS bytes of one gemv_nb_kernel workgroup (all static allocations)
-template <int NB, int D, int WAVES, int ROT, int NT = 1, bool RMS = false>
+template <int NB, int D, int WAVES, int ROT, int NT = 1, bool RMS = false, bool OVL = false>
 constexpr int nb_lds_bytes() {
     using P = NbSpec<NB, NT>;
     constexpr int act = (Q81_BYTES * P::NCH * NT + 1023) / 1024 * 1024;
     constexpr int ring = WAVES * (D + 1) * P::LDSB;
     constexpr int nhb = P::NCH / 32;
-    constexpr int stage = (ROT ? nhb * HBLK * 4 : 0) + (ROT == 2 ? nhb * HBLK * 4 : 0)   // ROT 3: x only
+    constexpr int stage = OVL ? 0 : (ROT ? nhb * HBLK * 4 : 0) + (ROT == 2 ? nhb * HBLK * 4 : 0)   // ROT 3: x only
                           + (RMS ? nhb * HBLK * 4 + 8 * WAVES : 0);
     return act + ring + stage;
 }
@@ -810,11 +856,12 @@ bool group_units(MatGroup & mg, int n_mat) {
     return u < 0x40000000;
 }
 
-template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, int NT = 1, bool RP = false, bool RMS = false>
+template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, int NT = 1, bool RP = false, bool RMS = false,
+          bool OVL = false>
 int launch_nb_t(MatGroup mg, int n_mat, const void * xin, const float * signs, int32_t * dump,
                 int per_cu, hipStream_t st, int n_tok = 1) {
     using P = NbSpec<NB, NT>;
-    constexpr int lds = nb_lds_bytes<NB, D, WAVES, ROT, NT, RMS>();
+    constexpr int lds = nb_lds_bytes<NB, D, WAVES, ROT, NT, RMS, OVL>();
     static_assert(lds <= LDS_PER_CU, "workgroup LDS");
     if (!group_units<P::G>(mg, n_mat)) return 1;
     const int n_units = mg.u0[MAX_GROUP];
@@ -834,7 +881,14 @@ int launch_nb_t(MatGroup mg, int n_mat, const void * xin, const float * signs, i
     int xl = env_int("BONSAI_GEMV_XCD_LOG2M", 2);
     if (xl < 0 || xl > 3 || blocks % 8 != 0) xl = 0;
     while (xl > 0 && ((blocks / 8) * WAVES) % (1 << xl) != 0) --xl;
-    if constexpr (RMS) {
+    if constexpr (OVL) {
+        if (n_mat > 1)
+            hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, ROT, true, 1, false, false, true>), dim3(blocks),
+                               dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl);
+        else
+            hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, ROT, false, 1, false, false, true>), dim3(blocks),
+                               dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl);
+    } else if constexpr (RMS) {
         if (n_mat > 1)
             hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, ROT, true, 1, false, true>), dim3(blocks),
                                dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl);
@@ -1123,6 +1177,10 @@ int launch_nb_rot(const MatGroup & mg, int n_mat, const float * x, const float *
     if (per_cu <= 0) per_cu = 1;
     if constexpr (nb_lds_bytes<NB, 2, 8, ROT, 1, RMS>() <= LDS_PER_CU) {
         if (waves == 8) return launch_nb_t<NB, 2, 8, false, ROT, 1, RP, RMS>(mg, n_mat, x, signs, nullptr, per_cu, st);
+    } else if constexpr (ROT == 1 && !RP && !RMS && nb_lds_bytes<NB, 2, 8, 1, 1, false, true>() <= LDS_PER_CU) {
+        // the separate stage does not fit beside an 8-wave ring: stage in the ring
+        if (waves == 8 && env_int("BONSAI_FGEMV_OVL", 1) == 1)
+            return launch_nb_t<NB, 2, 8, false, 1, 1, false, false, true>(mg, n_mat, x, signs, nullptr, per_cu, st);
     }
     if constexpr (nb_lds_bytes<NB, 2, 4, ROT, 1, RMS>() <= LDS_PER_CU)
         return launch_nb_t<NB, 2, 4, false, ROT, 1, RP, RMS>(mg, n_mat, x, signs, nullptr, per_cu, st);
