@@ -696,6 +696,26 @@ def test_rmsnorm_fwht_quant_bit_exact(n, n_tok, use_signs):
     np.testing.assert_array_equal(host(xq), exp)
 
 
+@pytest.mark.parametrize("n,n_tok", [(5120, 1), (1024, 4100)])
+def test_rmsnorm_fwht_quant_unaligned(n, n_tok):
+    """x and w one float past a 16-byte boundary (scalar loads), per-block and
+    per-token kernels: byte-exact against the same emulation."""
+    case(f"rmsnorm_fwht_quant unaligned n={n} n_tok={n_tok}")
+    X = (O.gen_normal(2700 + n, n_tok * n) * 2).reshape(n_tok, n)
+    w = O.gen_normal(2701 + n, n) * 0.1 + 1
+    xb = torch.zeros(n_tok * n + 4, dtype=torch.float32, device="cuda")
+    wb = torch.zeros(n + 4, dtype=torch.float32, device="cuda")
+    xb[1:1 + n_tok * n] = dev(X.reshape(-1))
+    wb[1:1 + n] = dev(w)
+    xq = torch.full((n // 32 * 36 * n_tok,), 0xAB, dtype=torch.uint8, device="cuda")
+    B.rmsnorm_fwht_quant(xb.data_ptr() + 4, wb.data_ptr() + 4, None, xq, n, n_tok, 1e-6)
+    s = np.array([rms_scale_fp64(X[t], 1e-6) for t in range(n_tok)], np.float32)
+    Y = ((X * s[:, None]).astype(np.float32) * w).astype(np.float32)
+    q = O.quantize_q8_1(O.fwht(Y.reshape(-1)), True)
+    exp = q.reshape(n_tok, n // 32, 36).transpose(1, 0, 2).reshape(-1)
+    np.testing.assert_array_equal(host(xq), exp)
+
+
 def test_rmsnorm_fwht_quant_against_reference_order():
     """Against the reference's own chain (sequential fp32 sum of squares,
     src/ops.h:13-22): the scales differ by that sum's rounding, so a few q
