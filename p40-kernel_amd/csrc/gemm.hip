@@ -641,6 +641,20 @@ int env_int_gemm(const char * name, int dflt) {
     return (v && *v) ? atoi(v) : dflt;
 }
 
+int gemm_cu_count() {
+    static int v = -1;
+    if (v < 0) {
+        int dev = 0, x = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&x, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || x <= 0) {
+            (void)hipGetLastError();
+            x = 256;
+        }
+        v = x;
+    }
+    return v;
+}
+
 int skinny_lds_limit() {
     static int v = -1;
     if (v < 0) {
@@ -686,9 +700,8 @@ int skinny_lds_limit() {
 //    v_perm spread 4 high bytes into 4 halves;
 //  * q -> f16(q): v_perm builds the halves 0x6400 + (q + 128) (= 1024 + q +
 //    128), a packed f16 add of -1152 leaves q.
-constexpr int GF_BM = 128, GF_BN = 128;
+constexpr int GF_BM = 128;
 constexpr int GF_STAGE_A = 4 * GF_BM * 64;          // bytes: [4 chunks][BM rows][64 B]
-constexpr int GF_STAGE_B = 4 * GF_BN * 64;
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
@@ -723,17 +736,22 @@ __device__ __forceinline__ void q4_to_f16(uint32_t q4, uint32_t & lo, uint32_t &
 // lanes per cycle) and with 64 banks (16 lanes per cycle).
 __device__ __forceinline__ int gf_swz(int r, int g) { return r * 64 + ((g ^ ((r >> 1) ^ (r >> 2))) & 3) * 16; }
 
-// WM x WN waves, each owning MI x NI MFMA tiles of 16 x 16 (the workgroup
-// tile is always 128 x 128).  With 512 threads every thread stages one A item
+// WM x WN waves, each owning MI x NI MFMA tiles of 16 x 16; the workgroup
+// tile is 128 rows x BN tokens (BN = 128, or 64 where the 128-token tiles
+// leave CUs idle).  With 512 threads (BN = 128) every thread stages one A item
 // and one B item per block; with 1024 threads (4 waves per SIMD, for latency
-// hiding) waves 0-7 stage A items and waves 8-15 B items.
-template <int WM, int WN, int MI, int NI>
+// hiding) waves 0-7 stage A items, the next BN / 16 waves B items, and the
+// rest only compute.
+template <int WM, int WN, int MI, int NI, int BN = 128>
 __global__ void __launch_bounds__(64 * WM * WN)
 gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
                 float * __restrict__ Y, int n_out, int n_tok, int nb) {
     constexpr int THREADS = 64 * WM * WN;
+    constexpr int GF_BN = BN;
+    constexpr int GF_STAGE_B = 4 * BN * 64;
     static_assert(16 * MI * WM == GF_BM && 16 * NI * WN == GF_BN, "workgroup tile");
     static_assert(THREADS == 512 || THREADS == 1024, "staging roles");
+    static_assert(BN == 128 || (BN == 64 && THREADS == 1024), "token tile");
     constexpr bool SPLIT = THREADS == 1024;
     __shared__ __attribute__((aligned(16))) uint8_t sA[2][GF_STAGE_A];
     __shared__ __attribute__((aligned(16))) uint8_t sB[2][GF_STAGE_B];
@@ -755,7 +773,7 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
     // LDS writes of a wave cover consecutive rows / tokens of one chunk
     const int it = tid & 511;
     const int ar = it & 127, ap = it >> 7;                     // a wave stages 64 consecutive rows
-    const int bp = it >> 7, bt = it & 127;
+    const int bp = it / BN, bt = it % BN;
 
     float acc[MI][NI][4];
 #pragma unroll
@@ -956,7 +974,8 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
     __syncthreads();
     if constexpr (!SPLIT) main_loop(yes{}, yes{});
     else if (wave < 8) main_loop(yes{}, no{});
-    else main_loop(no{}, yes{});
+    else if (wave < 8 + BN / 16) main_loop(no{}, yes{});
+    else main_loop(no{}, no{});
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
@@ -1021,12 +1040,23 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
         return (int)hipGetLastError();
     }
     if (env_int_gemm("BONSAI_GEMM_KERNEL", 0) == 0) {
-        dim3 grid((unsigned)cdiv(n_out, GF_BM), (unsigned)cdiv(n_tok, GF_BN));
         // 16 waves (4 per SIMD, 32 x 32 wave tiles) measured 12-22 % faster than
         // 8 waves (2 per SIMD, 64 x 32) on every prefill shape: the latency of
-        // the chunk pipeline and the per-block barrier is hidden by more waves
+        // the chunk pipeline and the per-block barrier is hidden by more waves.
+        // One workgroup fits a CU: where even twice the 128-token tiles fit in
+        // one round, 64-token tiles put twice the CUs to work (6144x5120 at
+        // M = 256: 61 -> 42 us); past that the extra round costs more than the
+        // idle CUs (5120x17408 at M = 512: 200 -> 256 us), so 128.
+        const int64_t tiles128 = cdiv(n_out, GF_BM) * cdiv(n_tok, 128);
+        int bn = env_int_gemm("BONSAI_GEMM_F16_BN", 0);
+        if (bn != 64 && bn != 128) bn = 2 * tiles128 <= gemm_cu_count() ? 64 : 128;
+        const dim3 grid((unsigned)cdiv(n_out, GF_BM), (unsigned)cdiv(n_tok, bn));
         if (env_int_gemm("BONSAI_GEMM_F16_WAVES", 16) == 8)
-            hipLaunchKernelGGL((gemm_f16_kernel<2, 4, 4, 2>), grid, dim3(512), 0, st, w, x, Y, (int)n_out, (int)n_tok, nb);
+            hipLaunchKernelGGL((gemm_f16_kernel<2, 4, 4, 2>), dim3(grid.x, (unsigned)cdiv(n_tok, 128)), dim3(512),
+                               0, st, w, x, Y, (int)n_out, (int)n_tok, nb);
+        else if (bn == 64)
+            hipLaunchKernelGGL((gemm_f16_kernel<4, 4, 2, 1, 64>), grid, dim3(1024), 0, st, w, x, Y, (int)n_out,
+                               (int)n_tok, nb);
         else
             hipLaunchKernelGGL((gemm_f16_kernel<4, 4, 2, 2>), grid, dim3(1024), 0, st, w, x, Y, (int)n_out, (int)n_tok, nb);
     } else if ((nb & 1) || ((uintptr_t)W & 3u) != 0) {

@@ -601,6 +601,23 @@ def test_gemm_large_block_scales_with_code3(waves, monkeypatch):
     assert normwise(host(y), O.gemv(W, xq, n_out, n_in)) <= TOL
 
 
+@pytest.mark.parametrize("bn", ["64", "128"])
+@pytest.mark.parametrize("n_out,n_in,n_tok", [(1000, 5120, 200), (300, 6144, 77), (129, 1024, 130)])
+def test_gemm_token_tile(bn, n_out, n_in, n_tok, monkeypatch):
+    """Both token tiles of the prefill kernel on ragged shapes (partial row
+    and token tiles), against the oracle."""
+    monkeypatch.setenv("BONSAI_GEMM_F16_BN", bn)
+    case(f"gemm {n_out}x{n_in}x{n_tok} token tile {bn}")
+    W = O.gen_weights(2800 + n_out, n_out, n_in)
+    X = O.gen_normal(2801 + n_tok, n_tok * n_in).reshape(n_tok, n_in)
+    Xq = O.quantize_chunk_major(X)
+    Y = torch.full((n_out, n_tok), float("nan"), dtype=torch.float32, device="cuda")
+    B.gemm(dev(W), dev(Xq), Y, n_out, n_in, n_tok)
+    got = host(Y)
+    assert np.all(np.isfinite(got))
+    assert normwise(got, O.gemm(W, Xq, n_out, n_in, n_tok, nthreads=16)) <= TOL
+
+
 def test_gemm_equals_gemv_per_token():
     case("gemm n_tok=3 equals three gemv")
     n_out, n_in, n_tok = 300, 5120, 3
