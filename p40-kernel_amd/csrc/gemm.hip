@@ -318,6 +318,7 @@ gemm_mfma_kernel_u16(const uint8_t * __restrict__ W, const uint8_t * __restrict_
 // K-quarter partials are summed through LDS.
 typedef int v2i __attribute__((ext_vector_type(2), aligned(4)));
 typedef int v4ia __attribute__((ext_vector_type(4)));
+typedef int v4ia4 __attribute__((ext_vector_type(4), aligned(4)));   // 4-byte aligned (36-byte records)
 typedef __attribute__((address_space(3))) void lds_void;
 
 __global__ void __launch_bounds__(256)
@@ -625,6 +626,232 @@ int launch_small_nt(const uint8_t * W, const uint8_t * X, float * Y, int n_out, 
     if (n_tok <= 4) return launch_small_t<RT, KS, 4>(W, X, Y, n_out, n_tok, nb, st);
     if (n_tok <= 8) return launch_small_t<RT, KS, 8>(W, X, Y, n_out, n_tok, nb, st);
     return launch_small_t<RT, KS, 16>(W, X, Y, n_out, n_tok, nb, st);
+}
+
+// ---------------------------------------------------------------------------
+// Small batch (3 <= n_tok <= 8) on v_mfma_i32_16x16x64_i8 with a
+// block-diagonal B.  The 16 MFMA columns are (token, chunk) pairs, not
+// tokens: with NT tokens a 16 x 16 result tile holds CPD = 16 / NT (rounded
+// down to 4 or 2) chunks of every token, so no column idles for want of
+// tokens and the per-chunk fp32 rescale runs once per 16 x 16 tile instead
+// of once per chunk.  One instruction has K = 64 = two chunks: K-group g of
+// lane (x, g) carries half g & 1 of chunk 2m + (g >> 1) of the tile; the A
+// lane (row x, g) holds those 16 codes (0..3, the code dword's bit pairs k
+// = 0..3 as four int8 dwords, (w >> 2k) & 0x03030303), the B lane (column x,
+// g) the 16 matching permuted activation bytes -- activation words 4h..4h+3
+// of half h line up with the four bit pairs of code dword h byte for byte --
+// when column x's chunk is that chunk, and 16 zero bytes otherwise.  A tile
+// takes CPD / 2 instructions accumulating into one result, started at -s of
+// each column's (token, chunk), so every element is exactly the chunk dot
+// sum (code - 1) q.  Lane (x, g) of the result holds rows 4g + i of column
+// x: inner += da(column) * S per tile, acc += dw(row, block) * inner per
+// block; the CPD columns of a token and the KS K-ranges meet in LDS at the
+// end.  Streaming as gemm_small_kernel: R = 16 RT rows per workgroup, K split
+// over KS waves in pieces of two blocks, each wave's pieces DMA'd through a
+// private two-slot LDS ring (weights and the pieces' NT-token activations).
+template <int NT>
+struct BdShape {
+    static constexpr int CPD = NT <= 4 ? 4 : 2;          // chunks per result tile
+    static constexpr int MPD = CPD / 2;                   // instructions per tile
+    static constexpr int DPB = 4 / CPD;                   // tiles per block
+    static constexpr int ZERO = 2048;                     // zero bytes behind the rings
+    static_assert(NT >= 3 && NT <= 8, "token count");
+    static_assert((8 - CPD) * NT * Q81_BYTES + 16 <= ZERO, "zero region covers every tile offset");
+};
+
+template <int RT, int KS, int NT>
+__global__ void __launch_bounds__(64 * KS)
+gemm_bd_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
+               float * __restrict__ Y, int n_out, int nb) {
+    using C = SkinnyCfg<RT, KS, NT>;
+    using S = BdShape<NT>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint8_t * ring = smem + (size_t)wave * SK_D * C::SLOT;
+    uint8_t * zero = smem + C::LDS;
+    for (int i = threadIdx.x; i < S::ZERO / 16; i += 64 * KS)
+        reinterpret_cast<v4ia *>(zero)[i] = (v4ia){0, 0, 0, 0};
+    const int row0 = blockIdx.x * C::R;
+    const size_t rs = (size_t)PQ2_BYTES * nb;
+    const int np_all = nb / 2;
+    const int pbeg = wave * np_all / KS, pend = (wave + 1) * np_all / KS;
+    const int np = pend - pbeg;                             // pieces of this wave (>= 1)
+    const int blk0 = 2 * pbeg;
+
+    uint32_t woff[C::NIW];
+#pragma unroll
+    for (int k = 0; k < C::NIW; ++k) {
+        const int idx = min(64 * k + lane, C::W_DW - 1);   // lanes past the piece re-read its last dword
+        const int r = idx / 17, d = idx - 17 * r;
+        woff[k] = (uint32_t)(min(row0 + r, n_out - 1) * rs + 4 * d);
+    }
+    uint32_t aoff[C::NIA];
+#pragma unroll
+    for (int k = 0; k < C::NIA; ++k) aoff[k] = 16u * (uint32_t)min(64 * k + lane, C::A_PC - 1);
+#define PQ2_BD_ISSUE(j, slot)                                                                      \
+    small_issue<C::NIW, C::NIA>(W + (size_t)PQ2_BYTES * (blk0 + 2 * (j)), woff,                      \
+                                X + (size_t)4 * (blk0 + 2 * (j)) * NT * Q81_BYTES, aoff,             \
+                                ring + (slot) * C::SLOT, C::W_BYTES)
+#pragma unroll
+    for (int i = 0; i < SK_D; ++i) PQ2_BD_ISSUE(min(i, np - 1), i);
+    __syncthreads();                                        // the zero region is written
+
+    const int x = lane & 15, g = lane >> 4;
+    const int gq = g >> 1, hh = g & 1;
+    const int cc = x / NT, t = x - NT * (x / NT);           // column x = chunk cc of token t
+    const bool col_ok = cc < S::CPD;
+    const int cce = col_ok ? cc : S::CPD - 1;               // idle columns read a live column's scale
+    // slot-relative byte offsets of the lane's B operand (before the tile's
+    // chunk offset) and of its column's Q8_1 scale word
+    const int b_off = C::W_BYTES + (cc * NT + t) * Q81_BYTES + 4 + 16 * hh;
+    const int ds_off = C::W_BYTES + (cce * NT + t) * Q81_BYTES;
+    const int a_off = x * 68 + 2 + 8 * gq + 4 * hh;         // code dword of (row x, K-group g), block 0 of the piece
+    float acc[RT][4];
+#pragma unroll
+    for (int mt = 0; mt < RT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[mt][i] = 0.0f;
+
+    for (int j = 0; j < np; ++j) {
+        const int slot = j % SK_D;
+        if (j + 1 < np) wait_vmcnt_sk<C::PER>(); else wait_vmcnt_sk<0>();
+        __builtin_amdgcn_wave_barrier();
+        const uint8_t * wl = ring + slot * C::SLOT;
+        // instruction m reads real activations only where column x's chunk is
+        // the chunk its K-group carries, zeros elsewhere
+        const uint8_t * bsrc[S::MPD];
+#pragma unroll
+        for (int m = 0; m < S::MPD; ++m) bsrc[m] = (col_ok && cc == 2 * m + gq) ? wl + b_off : zero;
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb) {
+            float inner[RT][4];
+#pragma unroll
+            for (int dt = 0; dt < S::DPB; ++dt) {
+                const int c0 = 4 * bb + dt * S::CPD;        // first chunk of the tile within the piece
+                const uint32_t dsw = *reinterpret_cast<const uint32_t *>(wl + ds_off + c0 * NT * Q81_BYTES);
+                const int ns = -(int)(int16_t)(dsw >> 16);
+                const float da = f16_bits_to_f32(dsw & 0xffffu);
+                v4ia Dt[RT];
+#pragma unroll
+                for (int mt = 0; mt < RT; ++mt) Dt[mt] = (v4ia){ns, ns, ns, ns};
+#pragma unroll
+                for (int m = 0; m < S::MPD; ++m) {
+                    const v4ia Bv = *reinterpret_cast<const v4ia4 *>(bsrc[m] + c0 * NT * Q81_BYTES);
+#pragma unroll
+                    for (int mt = 0; mt < RT; ++mt) {
+                        // code dword: chunk c0 + 2m + gq, half hh, row 16 mt + x (2-byte aligned in block 0)
+                        const int off = a_off + 16 * mt * 68 + 34 * bb + 8 * (dt * S::CPD + 2 * m);
+                        uint32_t w;
+                        if (bb == 0) {
+                            const uint32_t lo = *reinterpret_cast<const uint32_t *>(wl + off - 2);
+                            const uint32_t hi = *reinterpret_cast<const uint32_t *>(wl + off + 2);
+                            w = __builtin_amdgcn_alignbyte(hi, lo, 2);
+                        } else {
+                            w = *reinterpret_cast<const uint32_t *>(wl + off);
+                        }
+                        const v4ia Av = {(int)(w & 0x03030303u), (int)((w >> 2) & 0x03030303u),
+                                         (int)((w >> 4) & 0x03030303u), (int)((w >> 6) & 0x03030303u)};
+                        Dt[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(Av, Bv, Dt[mt], 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int mt = 0; mt < RT; ++mt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        inner[mt][i] = dt == 0 ? da * (float)Dt[mt][i] : fmaf(da, (float)Dt[mt][i], inner[mt][i]);
+            }
+            // block scale of rows 16 mt + 4g + i
+#pragma unroll
+            for (int mt = 0; mt < RT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t dwb = *reinterpret_cast<const uint16_t *>(wl + (16 * mt + 4 * g + i) * 68 + 34 * bb);
+                    acc[mt][i] = fmaf(f16_bits_to_f32(dwb), inner[mt][i], acc[mt][i]);
+                }
+        }
+        if (j + SK_D < np) {
+            __builtin_amdgcn_s_waitcnt(0xC07F);             // lgkmcnt(0): this slot's reads are done
+            __builtin_amdgcn_wave_barrier();
+            PQ2_BD_ISSUE(j + SK_D, slot);
+        }
+    }
+#undef PQ2_BD_ISSUE
+    // sum the CPD columns of every token and the KS K-ranges through LDS
+    __syncthreads();
+    float * red = reinterpret_cast<float *>(smem);            // [KS][R][16]
+#pragma unroll
+    for (int mt = 0; mt < RT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[(wave * C::R + 16 * mt + 4 * g + i) * 16 + x] = acc[mt][i];
+    __syncthreads();
+    for (int e = threadIdx.x; e < C::R * NT; e += 64 * KS) {
+        const int rr = e / NT, tt = e - NT * (e / NT);
+        float v = 0.0f;
+#pragma unroll
+        for (int q = 0; q < KS; ++q)
+#pragma unroll
+            for (int k = 0; k < S::CPD; ++k) v += red[(q * C::R + rr) * 16 + k * NT + tt];
+        const int row = row0 + rr;
+        if (row < n_out) Y[(size_t)row * NT + tt] = v;
+    }
+}
+
+template <int RT, int KS, int NT>
+int launch_bd_t(const uint8_t * W, const uint8_t * X, float * Y, int n_out, int nb, hipStream_t st) {
+    using C = SkinnyCfg<RT, KS, NT>;
+    constexpr int lds = C::LDS + BdShape<NT>::ZERO;
+    auto kern = gemm_bd_kernel<RT, KS, NT>;
+    static bool attr = false;
+    if (!attr) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+            (void)hipGetLastError();   // a refused request must not linger as the launch's error
+        attr = true;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(n_out, C::R)), dim3(64 * KS), lds, st, W, X, Y, n_out, nb);
+    return (int)hipGetLastError();
+}
+
+template <int RT, int KS>
+int launch_bd_nt(const uint8_t * W, const uint8_t * X, float * Y, int n_out, int n_tok, int nb, hipStream_t st) {
+    switch (n_tok) {
+        case 3: return launch_bd_t<RT, KS, 3>(W, X, Y, n_out, nb, st);
+        case 4: return launch_bd_t<RT, KS, 4>(W, X, Y, n_out, nb, st);
+        case 5: return launch_bd_t<RT, KS, 5>(W, X, Y, n_out, nb, st);
+        case 6: return launch_bd_t<RT, KS, 6>(W, X, Y, n_out, nb, st);
+        case 7: return launch_bd_t<RT, KS, 7>(W, X, Y, n_out, nb, st);
+        case 8: return launch_bd_t<RT, KS, 8>(W, X, Y, n_out, nb, st);
+        default: return -1;
+    }
+}
+
+// Workgroup shape of the block-diagonal kernel, 0 where another small-batch
+// kernel is faster.  Measured on MI355X (us, HIP-graph replay; previous path
+// = 4x4x4 MFMA kernel for 3..4 tokens on its widths, 16x16x32 kernel else):
+//                 previous  16 rows/8 ways  16/4  32/4  32/8
+//   17408x5120 B3   11.56     10.81        11.83 12.45 13.78
+//              B4   10.92     13.78        11.82 12.63 14.00
+//              B5   15.57     14.21        12.56 13.66 14.78
+//              B8   15.86     15.51        14.87 14.42 19.68
+//   5120x17408 B3   16.02     13.85        17.44 19.16 14.59
+//              B4   17.16     14.48        17.39 19.21 14.54
+//              B5   18.03     15.43        17.44 20.24 15.24
+//              B8   18.78     17.15        18.64 20.11 15.74
+//   6144x5120  B5    7.72      6.81         7.36  8.38  7.48
+//              B8    8.16      7.31         7.93  8.50  7.93
+//   5120x6144  B3    6.61      7.15         7.82  8.48  7.55
+//              B4    6.76      7.49         7.95  8.67  7.72
+//              B5    8.70      7.86         8.25  9.31  8.18
+//              B8    8.94      8.48         8.62  9.20  8.37
+// (1 = 16 rows / K in 8, 2 = 16 / 4, 3 = 32 / 4, 4 = 32 / 8)
+int bd_choice(int nb, int64_t n_out, int64_t n_tok) {
+    if (n_tok < 3 || n_tok > 8) return 0;
+    const bool mfma4_width = nb == 8 || nb == 40 || nb == 48;
+    if (mfma4_width && (n_tok == 4 || (n_tok == 3 && nb != 40))) return 0;
+    if (nb >= 96) return n_tok >= 5 ? 4 : 1;
+    if (n_out >= 12288 && n_tok >= 5) return n_tok >= 7 ? 3 : 2;
+    return 1;
 }
 
 template <int WM, int WN, int TM, int TN>
@@ -1010,6 +1237,17 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
     const uint8_t * w = (const uint8_t *)W;
     const uint8_t * x = (const uint8_t *)Xq;
     if (n_tok == 1) return bonsai_p40_gemv(W, Xq, Y, n_out, n_in, stream);   // chunk-major == token-major
+    const int bd_cfg = env_int_gemm("BONSAI_GEMM_BD", -1) < 0 ? bd_choice(nb, n_out, n_tok)
+                                                              : env_int_gemm("BONSAI_GEMM_BD", 0);
+    if (bd_cfg > 0 && n_tok >= 3 && n_tok <= 8 && nb % 2 == 0 && nb >= 16 && ((uintptr_t)W & 3u) == 0 &&
+        ((uintptr_t)Xq & 15u) == 0) {
+        switch (bd_cfg) {
+            case 2: return launch_bd_nt<1, 4>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
+            case 3: return launch_bd_nt<2, 4>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
+            case 4: return launch_bd_nt<2, 8>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
+            default: return launch_bd_nt<1, 8>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
+        }
+    }
     if (n_tok <= 4) {
         const int rc = pq2::gemv_small_batch(W, Xq, Y, n_out, n_in, n_tok, stream);
         if (rc >= 0) return rc;

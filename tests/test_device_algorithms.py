@@ -112,3 +112,107 @@ def test_round_half_away_identity():
     got = np.trunc(two).astype(np.int64) - np.trunc(p).astype(np.int64)
     ref = (np.sign(p.astype(np.float64)) * np.floor(np.abs(p.astype(np.float64)) + 0.5)).astype(np.int64)
     np.testing.assert_array_equal(got, ref)
+
+
+# ----------------------------------------------------------------------------
+# Small batch with a block-diagonal B (gemm_bd_kernel in csrc/gemm.hip): the
+# lane-level operand assembly of v_mfma_i32_16x16x64_i8, emulated in numpy.
+# A lane (row x, K-group g) and a B lane (column x, K-group g) meet byte for
+# byte (the instruction's A and B lane layouts are the same), so the
+# emulation pairs them directly; what it checks is which code bits and which
+# activation bytes each lane loads, the zero lanes, the -s start value and
+# the column -> (token, chunk) bookkeeping, against the oracle's integer
+# chunk dots and its GEMM.
+def _bd_piece_slot(W, X, n_tok, rows, piece, nb):
+    """LDS slot of one piece as the kernel's DMA fills it: each row's two
+    blocks (68 bytes), then the 8 chunks x n_tok Q8_1 blocks of the piece."""
+    rb = W.reshape(-1, nb * O.PQ2_BYTES)
+    w = np.concatenate([rb[r, 68 * piece:68 * piece + 68] for r in rows])
+    a = X.reshape(-1, n_tok * O.Q81_BYTES)[8 * piece:8 * piece + 8].ravel()
+    return w, a
+
+
+def _bd_emulate(W, X, n_out, nb, NT, R=16):
+    CPD = 4 if NT <= 4 else 2
+    lanes = np.arange(64)
+    x, g = lanes & 15, lanes >> 4
+    gq, hh = g >> 1, g & 1
+    cc, t = x // NT, x % NT
+    col_ok = cc < CPD
+    cce = np.where(col_ok, cc, CPD - 1)
+    y = np.zeros((n_out, NT), np.float32)
+    D_all = {}
+    for row0 in range(0, n_out, R):
+        rows = [min(row0 + r, n_out - 1) for r in range(R)]
+        acc = np.zeros((64, 4), np.float32)
+        for piece in range(nb // 2):
+            wl, al = _bd_piece_slot(W, X, NT, rows, piece, nb)
+            for bb in range(2):
+                inner = np.zeros((64, 4), np.float32)
+                for dt in range(4 // CPD):
+                    c0 = 4 * bb + dt * CPD
+                    rec = al.reshape(8, NT, O.Q81_BYTES)
+                    dsw = rec[c0 + cce, t]
+                    da = dsw[:, 0:2].copy().view(np.float16).astype(np.float32).ravel()
+                    s = dsw[:, 2:4].copy().view(np.int16).astype(np.int64).ravel()
+                    D = np.repeat(-s[:, None], 4, axis=1)          # lane (x, g): rows 4g+i, column x
+                    for m in range(CPD // 2):
+                        # A: 16 int8 per lane from one code dword
+                        off = x * 68 + 2 + 8 * gq + 4 * hh + 34 * bb + 8 * (dt * CPD + 2 * m)
+                        wd = np.array([int.from_bytes(wl[o:o + 4].tobytes(), "little") for o in off], np.uint64)
+                        A = np.stack([((wd >> np.uint64(2 * k)) & np.uint64(0x03030303)) for k in range(4)], 1)
+                        Ab = A.astype("<u4").view(np.uint8).reshape(64, 16).astype(np.int64)
+                        # B: the matching 16 activation bytes, or zeros
+                        live = col_ok & (cc == 2 * m + gq)
+                        boff = (cc * NT + t) * O.Q81_BYTES + 4 + 16 * hh + c0 * NT * O.Q81_BYTES
+                        Bb = np.zeros((64, 16), np.int64)
+                        for l in np.nonzero(live)[0]:
+                            Bb[l] = al[boff[l]:boff[l] + 16].view(np.int8)
+                        # D[r][c] += sum over g, bytes of A(r, g) * B(c, g)
+                        Ar = Ab.reshape(4, 16, 16)                 # [g][row][byte]
+                        Br = Bb.reshape(4, 16, 16)                 # [g][col][byte]
+                        full = np.einsum("grk,gck->rc", Ar, Br)
+                        for l in lanes:
+                            D[l] += full[4 * g[l]:4 * g[l] + 4, x[l]]
+                    D_all[(row0, piece, bb, dt)] = D.copy()
+                    Df = D.astype(np.float32)
+                    inner = (da[:, None] * Df) if dt == 0 else (da[:, None] * Df + inner).astype(np.float32)
+                dwr = np.array([[wl[(4 * g[l] + i) * 68 + 34 * bb:(4 * g[l] + i) * 68 + 34 * bb + 2].view(np.float16)[0]
+                                 for i in range(4)] for l in lanes], np.float32)
+                acc = (dwr * inner + acc).astype(np.float32)
+        for l in lanes:
+            if not col_ok[l]:
+                continue
+            for i in range(4):
+                r = row0 + 4 * g[l] + i
+                if r < n_out:
+                    y[r, t[l]] += acc[l, i]
+    return y, D_all
+
+
+@pytest.mark.parametrize("NT", [3, 4, 5, 8])
+def test_block_diagonal_small_batch_emulation(NT):
+    n_out, n_in = 20, 1024
+    nb = n_in // 128
+    W = O.gen_weights(4100 + NT, n_out, n_in, 0.05)
+    xs = [O.gen_normal(4200 + 7 * NT + t, n_in) for t in range(NT)]
+    Xt = [O.quantize_q8_1(v, True) for v in xs]
+    X = np.stack([q.reshape(-1, O.Q81_BYTES) for q in Xt], 1).ravel()   # chunk-major
+    y, D_all = _bd_emulate(W, X, n_out, nb, NT)
+    # every result element is one exact integer chunk dot of its (token, chunk)
+    dots = [O.chunk_dots(W, Xt[t], n_out, n_in) for t in range(NT)]
+    CPD = 4 if NT <= 4 else 2
+    for (row0, piece, bb, dt), D in D_all.items():
+        for l in range(64):
+            xx, gg = l & 15, l >> 4
+            c, tt = xx // NT, xx % NT
+            if c >= CPD:
+                continue
+            chunk = 8 * piece + 4 * bb + dt * CPD + c
+            for i in range(4):
+                r = row0 + 4 * gg + i
+                if r < n_out:
+                    assert D[l, i] == dots[tt][r, chunk]
+    ref = O.gemm(W, X, n_out, n_in, NT)
+    scale = float(np.max(np.abs(ref)))
+    assert float(np.max(np.abs(y - ref))) <= 1e-5 * scale

@@ -499,12 +499,14 @@ def test_gemm_prefill_shapes_row_sample(n_out, n_in, n_tok):
     (17408, 5120, 2), (6144, 5120, 3), (1025, 5120, 4), (5120, 6144, 2), (77, 6144, 4),
     (333, 1024, 3), (64, 10240, 2), (31, 12288, 2), (17407, 5120, 2), (5120, 17408, 2),
     (301, 17408, 3), (100, 17408, 4), (257, 12288, 4), (5120, 17408, 4)])
-def test_gemm_small_batch_streaming(n_out, n_in, n_tok):
-    """2 tokens run on the streaming GEMV kernel with per-token planes (3 on
-    the widths without a 4x4x4 kernel), 3..4 on the 4x4x4 MFMA kernel (4 on
-    the other widths on the 16x16 MFMA kernel):
-    against the oracle, and against one GEMV per token (bit-identical for 2
-    tokens, where the unit shape and the arithmetic are the GEMV's)."""
+def test_gemm_small_batch_streaming(n_out, n_in, n_tok, monkeypatch):
+    """With the block-diagonal kernel switched off: 2 tokens run on the
+    streaming GEMV kernel with per-token planes (3 on the widths without a
+    4x4x4 kernel), 3..4 on the 4x4x4 MFMA kernel (4 on the other widths on
+    the 16x16 MFMA kernel): against the oracle, and against one GEMV per
+    token (bit-identical for 2 tokens, where the unit shape and the
+    arithmetic are the GEMV's)."""
+    monkeypatch.setenv("BONSAI_GEMM_BD", "0")
     case(f"gemm small batch {n_out}x{n_in}x{n_tok}")
     W = O.gen_weights(1400 + n_out + n_tok, n_out, n_in)
     X = np.stack([O.fwht(O.gen_normal(1401 + t + n_in, n_in)) for t in range(n_tok)])
@@ -528,13 +530,42 @@ def test_gemm_small_batch_streaming(n_out, n_in, n_tok):
 @pytest.mark.parametrize("n_out,n_in,n_tok", [
     (17408, 5120, 4), (17408, 5120, 3), (6144, 5120, 4), (5121, 6144, 3), (33, 1024, 4),
     (17407, 5120, 4), (1026, 6144, 4), (7, 5120, 3), (4095, 5120, 4), (4096, 5120, 3)])
-def test_gemm_small_batch_mfma4(n_out, n_in, n_tok):
+def test_gemm_small_batch_mfma4(n_out, n_in, n_tok, monkeypatch):
     """3..4 tokens on the 4x4x4 MFMA streaming kernel (4- and 8-wave
-    workgroups either side of 4096 rows): against the oracle and against one
-    GEMV per token."""
+    workgroups either side of 4096 rows; the block-diagonal kernel switched
+    off): against the oracle and against one GEMV per token."""
+    monkeypatch.setenv("BONSAI_GEMM_BD", "0")
     case(f"gemm small batch (mfma4) {n_out}x{n_in}x{n_tok}")
     W = O.gen_weights(1600 + n_out + n_tok, n_out, n_in)
     X = np.stack([O.fwht(O.gen_normal(1601 + t + n_in, n_in)) for t in range(n_tok)])
+    Xq = O.quantize_chunk_major(X)
+    Wd = dev(W)
+    Y = torch.full((n_out, n_tok), float("nan"), dtype=torch.float32, device="cuda")
+    B.gemm(Wd, dev(Xq), Y, n_out, n_in, n_tok)
+    got = host(Y)
+    assert np.all(np.isfinite(got))
+    assert normwise(got, O.gemm(W, Xq, n_out, n_in, n_tok, nthreads=16)) <= TOL
+    for t in range(n_tok):
+        y = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+        B.gemv(Wd, dev(O.quantize_q8_1(X[t], True)), y, n_out, n_in)
+        assert normwise(got[:, t], host(y)) <= 2 * TOL
+
+
+@pytest.mark.parametrize("cfg", ["auto", "1", "2", "3", "4"])
+@pytest.mark.parametrize("n_out,n_in,n_tok", [
+    (17408, 5120, 8), (5120, 17408, 4), (6144, 5120, 5), (1000, 6144, 6), (77, 2048, 7),
+    (33, 17408, 3), (5121, 12288, 8), (17, 10240, 4), (17408, 5120, 3), (5120, 6144, 8)])
+def test_gemm_small_batch_block_diagonal(n_out, n_in, n_tok, cfg, monkeypatch):
+    """3..8 tokens on the block-diagonal 16x16x64 MFMA kernel in each of its
+    workgroup shapes (16 or 32 rows, K split 4 or 8 ways) and through the
+    default choice: against the oracle and against one GEMV per token."""
+    if cfg == "auto":
+        monkeypatch.delenv("BONSAI_GEMM_BD", raising=False)
+    else:
+        monkeypatch.setenv("BONSAI_GEMM_BD", cfg)
+    case(f"gemm small batch (block-diagonal cfg {cfg}) {n_out}x{n_in}x{n_tok}")
+    W = O.gen_weights(1900 + n_out + n_tok, n_out, n_in)
+    X = np.stack([O.fwht(O.gen_normal(1901 + t + n_in, n_in)) for t in range(n_tok)])
     Xq = O.quantize_chunk_major(X)
     Wd = dev(W)
     Y = torch.full((n_out, n_tok), float("nan"), dtype=torch.float32, device="cuda")
