@@ -218,6 +218,25 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 // cache-policy operand of global_load_lds on gfx950: bit 1 = nt (non-temporal)
 constexpr int CPOL_NT = 2;
+// word 3 of a raw buffer descriptor on gfx9-family parts (32-bit data format,
+// no swizzle): byte-addressed loads with the range check against num_records
+constexpr int BUF_DW3 = 0x00020000;
+
+// NPL 16-byte LDS-DMA pieces of one unit from a matrix of m_bytes bytes (the
+// buffer range): piece k of lane l from byte unit_off + poff[k] into
+// dst + 1024 k + 16 l; pieces past the range land as zeros.  (A free
+// function: the buffer builtins inside a kernel lambda drop the kernel's
+// host-side stub.)
+template <int NPL>
+__device__ __forceinline__ void unit_buffer_dma(const uint8_t * W, int m_bytes, uint32_t unit_off,
+                                                const uint32_t * poff, uint8_t * dst) {
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(W), (short)0, m_bytes, BUF_DW3);
+#pragma unroll
+    for (int k = 0; k < NPL; ++k)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void *)(dst + 1024 * k), 16, unit_off + poff[k], 0, 0,
+                                                 CPOL_NT);
+}
 
 // Reduce acc0 over lanes 0..63 and acc1 over lanes 0..63 at once:
 // v_permlane32_swap folds the upper half of acc0 onto its lower half and the
@@ -479,6 +498,14 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         float * ym;
         int n_out_m, lu;
         gs.at(uu, Wm, ym, n_out_m, lu);
+        const uint64_t m_bytes = (uint64_t)n_out_m * (PQ2_BYTES * NB);
+        if (m_bytes < 0x80000000ull) {
+            // buffer DMA with the matrix as the range: the unit offset is one
+            // add per piece, and a piece past the end (a trailing unit with
+            // fewer than G rows) reads zeros instead of memory
+            unit_buffer_dma<P::NPL>(Wm, (int)m_bytes, (uint32_t)lu * (uint32_t)P::UB, poff, ring[slot]);
+            return;
+        }
         const uint8_t * base = Wm + (size_t)lu * P::UB;
         const bool full = lu < n_out_m / P::G;              // all G rows present
         const size_t last_piece = (size_t)n_out_m * PQ2_BYTES * NB / 16 - 1;
