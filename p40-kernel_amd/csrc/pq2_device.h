@@ -182,7 +182,10 @@ __device__ __forceinline__ void code_nibbles(uint32_t w0, uint32_t w1, uint32_t 
 
 __device__ __forceinline__ int chunk_dot_nibw(const uint32_t (&n)[4], const uint32_t (&h)[4],
                                               const uint32_t (&l)[4], int bias) {
-    int sh = __builtin_amdgcn_sdot8((int)n[0], (int)h[0], 0, false);
+    // the first product in the three-operand form with a literal 0 accumulator
+    // (the builtin becomes the tied-accumulator form plus a v_mov of the 0)
+    int sh;
+    asm("v_dot8_i32_i4 %0, %1, %2, 0" : "=v"(sh) : "v"(n[0]), "v"(h[0]));
     sh = __builtin_amdgcn_sdot8((int)n[1], (int)h[1], sh, false);
     sh = __builtin_amdgcn_sdot8((int)n[2], (int)h[2], sh, false);
     sh = __builtin_amdgcn_sdot8((int)n[3], (int)h[3], sh, false);
