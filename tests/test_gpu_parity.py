@@ -579,6 +579,26 @@ def test_gemm_small_batch_block_diagonal(n_out, n_in, n_tok, cfg, monkeypatch):
         assert normwise(got[:, t], host(y)) <= 2 * TOL
 
 
+@pytest.mark.parametrize("xl", ["0", "1", "2", "3"])
+@pytest.mark.parametrize("n_out,n_in", [(17408, 5120), (5120, 17408), (6144, 5120), (1000, 5120)])
+def test_gemv_xcd_unit_numbering(n_out, n_in, xl, monkeypatch):
+    """Every XCD grouping of the unit numbering (2^xl consecutive units per
+    XCD) covers each unit once: against the oracle and bit-identical to the
+    plain numbering (the unit shape and the arithmetic do not change)."""
+    case(f"gemv {n_out}x{n_in} XCD group 2^{xl}")
+    W, xq = make(n_out, n_in, 3100 + n_out + n_in)
+    Wd, xd = dev(W), dev(xq)
+    monkeypatch.setenv("BONSAI_GEMV_XCD_LOG2M", xl)
+    y = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+    B.gemv(Wd, xd, y, n_out, n_in)
+    got = host(y)
+    assert normwise(got, O.gemv(W, xq, n_out, n_in, nthreads=16)) <= TOL
+    monkeypatch.setenv("BONSAI_GEMV_XCD_LOG2M", "0")
+    y0 = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+    B.gemv(Wd, xd, y0, n_out, n_in)
+    np.testing.assert_array_equal(bits(got), bits(host(y0)))
+
+
 def test_gemm_subnormal_and_zero_block_scales():
     """Blocks whose fp16 scale is subnormal or zero (the prefill kernel
     multiplies the scale into its f16 operand)."""
