@@ -1,8 +1,8 @@
 #!/usr/bin/env python3
 """Benchmark of the gfx950 PQ2_0 matmul path (one MI355X).
 
-Headline (BASELINE.json metric): decode GEMV GB/s at 17408x5120 (config 1's
-gate/up shape), batch 1.  A "step" is one bonsai_p40_gemv over one
+Headline metric: decode GEMV GB/s at 17408x5120 (config 1's gate/up shape),
+batch 1.  A "step" is one bonsai_p40_gemv over one
 17408x5120 PQ2_0 matrix with an already-quantised activation resident in HBM.
 The weights rotate through enough distinct copies (>= 1.1 GB) that every step
 streams its matrix from HBM rather than from the 256 MB Infinity Cache.
@@ -353,7 +353,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the PQ2_0 path would shard by rows; see DESIGN.md)", file=sys.stderr)
+              "(the PQ2_0 path would shard by weight rows, with the activation "
+              "replicated and the outputs all-gathered)", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("no GPU visible", file=sys.stderr)
