@@ -226,9 +226,21 @@ def bench_ffn_chain(steps, warmup, gen):
         B.swiglu_fwht_quant(g, u, None, hq, N_FF)
         B.gemv(Wd, hq, y, N_EMBD, N_FF)
 
+    def step_grouped(i):
+        Wg, Wu, Wd = sets[i % R]
+        B.fwht_gemv_group([Wg, Wu], x, None, [g, u], [N_FF, N_FF], N_EMBD)
+        B.swiglu_fwht_quant(g, u, None, hq, N_FF)
+        B.gemv(Wd, hq, y, N_EMBD, N_FF)
+
+    def gate_up(i):
+        Wg, Wu, _ = sets[i % R]
+        B.gemv_group([Wg, Wu], xq, [g, u], [N_FF, N_FF], N_EMBD)
+
     ms = time_loop(step, steps, warmup)
+    ms_grouped = time_loop(step_grouped, steps, warmup)
+    ms_gu = time_loop(gate_up, steps, warmup)
     del sets, base
-    return ms, per + 0  # weight bytes per chain
+    return ms, per, ms_grouped, ms_gu  # weight bytes per chain
 
 
 def bench_token_sweep(steps, warmup, gen, mode="separate"):
@@ -448,9 +460,20 @@ def main():
                 "note": "fp32 activation in: FWHT + Q8_1 + GEMV in one launch (bonsai_p40_fwht_gemv)"}
             print(f"[bench] fwht_gemv {n_out}x{n_in}: {extra[f'fwht_gemv_{n_out}x{n_in}']}",
                   file=sys.stderr, flush=True)
-        m, wb = bench_ffn_chain(max(20, args.steps // 4), 5, gen)
-        extra["ffn_chain_config1"] = {"us": round(m * 1e3, 2), "weight_GB/s": round(wb / (m * 1e-3) / 1e9, 1)}
+        m, wb, mg, mgu = bench_ffn_chain(max(20, args.steps // 4), 5, gen)
+        extra["ffn_chain_config1"] = {"us": round(m * 1e3, 2), "weight_GB/s": round(wb / (m * 1e-3) / 1e9, 1),
+                                      "note": "pre-pass, gate GEMV, up GEMV, SwiGLU+FWHT+Q8_1, down GEMV"}
+        extra["ffn_chain_config1_grouped"] = {
+            "us": round(mg * 1e3, 2), "weight_GB/s": round(wb / (mg * 1e-3) / 1e9, 1),
+            "note": "gate+up as one fused grouped launch from fp32 x, SwiGLU+FWHT+Q8_1, down GEMV"}
+        gu_bytes = 2 * gemv_bytes(N_FF, N_EMBD) - B.q8_bytes(N_EMBD)
+        extra["gemv_group_gate_up_2x17408x5120"] = {
+            "us": round(mgu * 1e3, 3), "GB/s": round(gu_bytes / (mgu * 1e-3) / 1e9, 1),
+            "frac_hbm_peak": round(gu_bytes / (mgu * 1e-3) / 1e9 / 8000.0, 4),
+            "note": "config 1's gate and up GEMVs as one grouped launch (bonsai_p40_gemv_group)"}
         print(f"[bench] ffn chain: {extra['ffn_chain_config1']}", file=sys.stderr, flush=True)
+        print(f"[bench] ffn chain grouped: {extra['ffn_chain_config1_grouped']}", file=sys.stderr, flush=True)
+        print(f"[bench] gate+up grouped: {extra['gemv_group_gate_up_2x17408x5120']}", file=sys.stderr, flush=True)
         m, wb = bench_token_sweep(5, 2, gen)
         extra["token_sweep_config2"] = {"ms_per_token": round(m, 3), "tok/s": round(1e3 / m, 2),
                                         "weight_GB/s": round(wb / (m * 1e-3) / 1e9, 1),
