@@ -1288,6 +1288,27 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
         const int64_t tiles128 = cdiv(n_out, GF_BM) * cdiv(n_tok, 128);
         int bn = env_int_gemm("BONSAI_GEMM_F16_BN", 0);
         if (bn != 64 && bn != 128) bn = 2 * tiles128 <= gemm_cu_count() ? 64 : 128;
+        // A last round that only part-fills the CUs (17408 rows at M = 512:
+        // 544 tiles = 2 rounds + 32 tiles) costs a whole round.  Where the
+        // full rounds cover whole row tiles, they run as one launch and the
+        // remaining rows as a second launch of 64-token tiles, which spreads
+        // them over more CUs (twice the tiles, each about half the work).
+        const int cus = gemm_cu_count();
+        const int64_t ttok = cdiv(n_tok, 128), rounds = tiles128 / cus, rest = tiles128 - rounds * cus;
+        if (bn == 128 && rounds >= 1 && rest > 0 && 2 * rest <= cus && (rounds * cus) % ttok == 0 &&
+            env_int_gemm("BONSAI_GEMM_F16_SPLIT", 1) > 0 && env_int_gemm("BONSAI_GEMM_F16_WAVES", 16) != 8) {
+            const int64_t rows_main = rounds * cus / ttok * GF_BM;
+            const int64_t rows_tail = n_out - rows_main;
+            if (rows_tail > 0 && cdiv(rows_tail, GF_BM) * cdiv(n_tok, 64) <= cus) {
+                hipLaunchKernelGGL((gemm_f16_kernel<4, 4, 2, 2>), dim3((unsigned)(rows_main / GF_BM), (unsigned)ttok),
+                                   dim3(1024), 0, st, w, x, Y, (int)rows_main, (int)n_tok, nb);
+                hipLaunchKernelGGL((gemm_f16_kernel<4, 4, 2, 1, 64>),
+                                   dim3((unsigned)cdiv(rows_tail, GF_BM), (unsigned)cdiv(n_tok, 64)), dim3(1024), 0,
+                                   st, w + (size_t)rows_main * PQ2_BYTES * nb, x, Y + (size_t)rows_main * n_tok,
+                                   (int)rows_tail, (int)n_tok, nb);
+                return (int)hipGetLastError();
+            }
+        }
         const dim3 grid((unsigned)cdiv(n_out, GF_BM), (unsigned)cdiv(n_tok, bn));
         if (env_int_gemm("BONSAI_GEMM_F16_WAVES", 16) == 8)
             hipLaunchKernelGGL((gemm_f16_kernel<2, 4, 4, 2>), dim3(grid.x, (unsigned)cdiv(n_tok, 128)), dim3(512),

@@ -669,6 +669,33 @@ def test_gemm_token_tile(bn, n_out, n_in, n_tok, monkeypatch):
     assert normwise(got, O.gemm(W, Xq, n_out, n_in, n_tok, nthreads=16)) <= TOL
 
 
+@pytest.mark.parametrize("n_out,n_in,n_tok", [(17408, 5120, 512), (5120, 17408, 1024), (17408, 5120, 300)])
+def test_gemm_split_last_round(n_out, n_in, n_tok, monkeypatch):
+    """Where the 128-token tiles leave a part-filled last round, the rows of
+    the full rounds and the remaining rows run as two launches (128- and
+    64-token tiles): y is bit-identical to the single launch, and the rows
+    either side of the split match the oracle."""
+    case(f"gemm {n_out}x{n_in}x{n_tok} split last round")
+    W = O.gen_weights(3300 + n_out, n_out, n_in)
+    X = np.stack([O.fwht(O.gen_normal(3301 + t, n_in)) for t in range(n_tok)])
+    Xq = O.quantize_chunk_major(X)
+    Wd, Xd = dev(W), dev(Xq)
+    got = {}
+    for split in ("1", "0"):
+        monkeypatch.setenv("BONSAI_GEMM_F16_SPLIT", split)
+        Y = torch.full((n_out, n_tok), float("nan"), dtype=torch.float32, device="cuda")
+        B.gemm(Wd, Xd, Y, n_out, n_in, n_tok)
+        got[split] = host(Y)
+    assert np.all(np.isfinite(got["1"]))
+    np.testing.assert_array_equal(bits(got["1"]), bits(got["0"]))
+    cut = 16384 if n_out == 17408 else 4096
+    rows = np.r_[cut - 40:cut + 40]
+    rb = n_in // 128 * 34
+    Ws = np.concatenate([W[r * rb:(r + 1) * rb] for r in rows])
+    ref = O.gemm(Ws, Xq, rows.size, n_in, n_tok, nthreads=16)
+    assert normwise(got["1"][rows], ref) <= TOL
+
+
 def test_gemm_equals_gemv_per_token():
     case("gemm n_tok=3 equals three gemv")
     n_out, n_in, n_tok = 300, 5120, 3
