@@ -949,7 +949,18 @@ int launch_nb(const MatGroup & mg, int n_mat, const uint8_t * xq, int32_t * dump
     // 4-wave workgroups with two unit buffers per wave measured best at every
     // model width (deeper rings queue more bytes ahead of the activation)
     int per_cu = env_int("BONSAI_GEMV_WG_PER_CU", 0);
-    if (per_cu <= 0) per_cu = default_wg_per_cu(NB, group_weight_bytes(mg, n_mat, NB));
+    if (per_cu <= 0) {
+        per_cu = default_wg_per_cu(NB, group_weight_bytes(mg, n_mat, NB));
+        // a matrix below 16 MB whose units fill one 4-wave workgroup per CU
+        // evenly, with at most 3 units per wave, runs best that way (6144x5120:
+        // 3 units per wave, 4.41 -> 4.21 us, against 1.5 with two workgroups per
+        // CU; at 4 units per wave (q/k/v grouped: 4.80 -> 5.11 us) and 5
+        // (5120x6144) two workgroups per CU stay faster)
+        int64_t units = 0;
+        for (int m = 0; m < n_mat; ++m) units += (mg.n_out[m] + NbSpec<NB, 1>::G - 1) / NbSpec<NB, 1>::G;
+        const int64_t waves1 = 4 * (int64_t)cu_count();
+        if (per_cu == 2 && units % waves1 == 0 && units / waves1 <= 3) per_cu = 1;
+    }
     return launch_nb_t<NB, 2, 4, DUMP>(mg, n_mat, xq, nullptr, dump, per_cu, st);
 }
 
