@@ -4,6 +4,9 @@
 // boetti-dev/p40-kernel: every declaration of that header is kept with the
 // same name, argument order, argument meaning and return-code convention, so
 // C++ host code written against it links against libbonsai_p40.so unchanged.
+// Where the reference's host and device code disagree, the reference name
+// keeps what the reference LIBRARY does when it reads memory (the FWHT's
+// 1024-entry signs), and its rounding follows the host code (below).
 // The library is written for AMD CDNA4 (gfx950) in HIP; `bonsai_stream` is a
 // hipStream_t (NULL = the default stream).
 //
@@ -74,11 +77,14 @@ int bonsai_p40_gemv_repack(const void * W, const float * x, float * y,
                            int64_t n_out, int64_t n_in, bonsai_stream stream);
 
 // --- transforms -----------------------------------------------------------------
-// In-place normalised Sylvester-Hadamard transform in blocks of 1024, signs
-// (optional, NULL = all +1) a length-n vector: block b uses signs[1024b ..]
-// (the host form, src/fwht.h:38-42).  Stage order h = 1..512 as the host, so
-// the result is bit-identical to fwht_blocks().  Errors: 1 if n <= 0 or
-// n % 1024 != 0.  Replaces include/bonsai_p40.h:41 (elementwise_p40.cu:75-80).
+// In-place normalised Sylvester-Hadamard transform in blocks of 1024.  signs
+// (optional, NULL = all +1) has 1024 entries, used by EVERY block: the meaning
+// of the reference device kernel (elementwise_p40.cu:17-41, signs[i] with
+// i < 1024), so a buffer sized for the reference library is never read past.
+// Stage order h = 1..512 as the host, so the result is bit-identical to the
+// host fwht_blocks() given that vector tiled to length n.  Errors: 1 if
+// n <= 0 or n % 1024 != 0.  Replaces include/bonsai_p40.h:41
+// (elementwise_p40.cu:75-80).
 int bonsai_p40_fwht(float * x, const float * signs, int64_t n, bonsai_stream stream);
 
 // Not on the PQ2_0 matmul path; kept so the reference's symbol set links.
@@ -95,6 +101,14 @@ int bonsai_p40_attn(const float * q, const float * k, const float * v, float * o
                     bonsai_stream stream);
 
 // --- additions (no counterpart in the reference header) -------------------------
+// Every addition that takes `signs` reads a length-n vector (block b uses
+// signs[1024 b ..]), the host form of src/fwht.h:38-42.
+
+// bonsai_p40_fwht with the host's length-n signs (block b uses
+// signs[1024 b .. 1024 b + 1023]): bit-identical to fwht_blocks(x, signs, n).
+// Errors as bonsai_p40_fwht.
+int bonsai_p40_fwht_signs_n(float * x, const float * signs, int64_t n, bonsai_stream stream);
+
 // Fused decode pre-pass: xq = Q8_1(FWHT(signs .* x)) for one token of n floats
 // (x is not modified).  One launch in place of bonsai_p40_fwht followed by
 // bonsai_p40_quant_activations (elementwise_p40.cu:17-41 + gemv_p40.cu:168-196),
@@ -176,11 +190,30 @@ int bonsai_p40_rmsnorm_fwht_gemv_group(const void * const * W, float * const * y
                                        int n_mat, const float * x, const float * norm_w, const float * signs,
                                        int64_t n_in, float eps, bonsai_stream stream);
 
+// Reference ternary weight quantiser: n fp32 weights (n % 128 == 0, rows of a
+// matrix back to back) -> n/128 block_pq2_0 with d = amax rounded to fp16
+// half away from zero and code = clamp(lroundf(x / amax) + 1, 0, 3); bytes
+// equal quantize_row_pq2_0 (src/pq2_0.h:74-90) for finite inputs.  A
+// load-time transform; the reference has it only on the host.  Errors: 1 if
+// n <= 0, n % 128 != 0, a pointer is NULL, x is not 4-byte or w not 2-byte
+// aligned.
+int bonsai_p40_quantize_pq2_0(const float * x, void * w, int64_t n, bonsai_stream stream);
+// Its inverse: y = (code - 1) * d for n weights (src/pq2_0.h:62-71), exact.
+// Errors as bonsai_p40_quantize_pq2_0.
+int bonsai_p40_dequantize_pq2_0(const void * w, float * y, int64_t n, bonsai_stream stream);
+
 // Test hook: out[r * (n_in/32) + c] = the int32 chunk dot sum_k (code-1)*q of
 // row r, chunk c, computed by the same device code path as bonsai_p40_gemv
 // (the value of src/pq2_0.h:149-177 before scaling).  Errors as bonsai_p40_gemv.
 int bonsai_p40_chunk_dots(const void * W, const void * xq, int32_t * out,
                           int64_t n_out, int64_t n_in, bonsai_stream stream);
+
+// Tuning hook: the library reads its BONSAI_* environment variables (kernel
+// variant selectors used by tests and sweeps) once per process, at the first
+// call that needs one; this re-reads them after a caller changed them.
+// Thread-safe; launches already enqueued keep the variants they were given.
+// Returns 0.
+int bonsai_p40_reload_tuning(void);
 
 // Measurement helper: a streaming read of `bytes` (16-byte aligned, multiple
 // of 16) with `blocks` workgroups of 256 lanes -- the achievable-HBM-bandwidth

@@ -59,6 +59,7 @@ def lib():
         L.orc_fwht_blocks.argtypes = [_f32p, _f32p, _i64]
         L.orc_dequantize_pq2_0.argtypes = [_u8p, _f32p, _i64]
         L.orc_quantize_pq2_0.argtypes = [_f32p, _u8p, _i64]
+        L.orc_pq2_0_dot_f32.argtypes = [_u8p, _f32p]; L.orc_pq2_0_dot_f32.restype = C.c_float
         L.orc_chunk_sumi.argtypes = [_u8p, _u8p, C.c_int]; L.orc_chunk_sumi.restype = C.c_int32
         L.orc_row_dot.argtypes = [_u8p, _u8p, _i64]; L.orc_row_dot.restype = C.c_float
         L.orc_gemv.argtypes = [_u8p, _u8p, _f32p, _i64, _i64, C.c_int]
@@ -90,6 +91,7 @@ def ref():
         R.ref_fwht_blocks.argtypes = [_f32p, _f32p, _i64]
         R.ref_quantize_pq2_0.argtypes = [_f32p, _u8p, _i64]
         R.ref_dequantize_pq2_0.argtypes = [_u8p, _f32p, _i64]
+        R.ref_pq2_0_dot_f32.argtypes = [_u8p, _f32p]; R.ref_pq2_0_dot_f32.restype = C.c_float
         R.ref_chunk_sumi.argtypes = [_u8p, _u8p, C.c_int]; R.ref_chunk_sumi.restype = C.c_int32
         R.ref_row_dot.argtypes = [_u8p, _u8p, _i64]; R.ref_row_dot.restype = C.c_float
         R.ref_gemv.argtypes = [_u8p, _u8p, _f32p, _i64, _i64]
@@ -146,6 +148,17 @@ def quantize_pq2_0(x: np.ndarray) -> np.ndarray:
     w = np.empty(x.size // QK_PQ2 * PQ2_BYTES, np.uint8)
     lib().orc_quantize_pq2_0(_p(x, _f32p), _p(w, _u8p), x.size)
     return w
+
+
+def pq2_0_dot_f32(W: np.ndarray, a: np.ndarray) -> np.ndarray:
+    """Float dot of every 34-byte block of W with its 128 floats of a
+    (a.size == 128 * blocks): one value per block."""
+    W = np.ascontiguousarray(W, np.uint8); a = np.ascontiguousarray(a, np.float32)
+    nblk = W.size // PQ2_BYTES
+    assert a.size == nblk * QK_PQ2
+    L = lib()
+    return np.array([L.orc_pq2_0_dot_f32(_p(W[b * PQ2_BYTES:], _u8p), _p(a[b * QK_PQ2:], _f32p))
+                     for b in range(nblk)], np.float32)
 
 
 def gemv(W: np.ndarray, xq: np.ndarray, n_out: int, n_in: int, nthreads: int = 1) -> np.ndarray:

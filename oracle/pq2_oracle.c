@@ -22,6 +22,10 @@
  *   orc_gemm            -- F6 fixtures + double-precision dequantised reference
  *   orc_swiglu          -- F7 fixtures (chain) within expf ulp tolerance
  *   orc_rmsnorm         -- F8 fixtures (bit patterns) + float64 closed form
+ *   orc_quantize_pq2_0  -- F9 fixture (lroundf ties, zero, fp16-tie, subnormal
+ *                          and overflowing scales) + closed form
+ *   orc_dequantize_pq2_0-- F9 fixture (bit patterns, code 3) + value rule
+ *   orc_pq2_0_dot_f32   -- F9 fixture (bit patterns) + float64 dot
  */
 #include <math.h>
 #include <stdint.h>
@@ -189,6 +193,20 @@ void orc_quantize_pq2_0(const float *x, uint8_t *w, int64_t k) {
             blk[2 + (j >> 2)] |= (uint8_t)(q << ((j & 3) * 2));
         }
     }
+}
+
+/* ---- float block dot: src/pq2_0.h:134-142 -------------------------------
+ * the definition every kernel reproduces: sum_j (code_j - 1) * a[j] in
+ * element order (fp32, no contraction), then times the block scale.      */
+float orc_pq2_0_dot_f32(const uint8_t *w, const float *a) {
+    const float d = orc_f16_to_f32(ld16(w));
+    float acc = 0.0f;
+    for (int j = 0; j < QK_PQ2; ++j) {
+        const int code = (w[2 + (j >> 2)] >> ((j & 3) * 2)) & 3;
+        volatile float prod = (float)(code - 1) * a[j];
+        acc += prod;
+    }
+    return acc * d;
 }
 
 /* ---- integer chunk dot: src/pq2_0.h:149-172 ------------------------------

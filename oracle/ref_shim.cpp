@@ -36,6 +36,10 @@ void ref_fwht_blocks(float * x, const float * signs, int64_t n) { fwht_blocks(x,
 
 void ref_quantize_pq2_0(const float * x, void * w, int64_t k) { quantize_row_pq2_0(x, (block_pq2_0 *)w, k); }
 void ref_dequantize_pq2_0(const void * w, float * y, int64_t k) { dequantize_row_pq2_0((const block_pq2_0 *)w, y, k); }
+float ref_pq2_0_dot_f32(const void * w, const float * a) {
+    block_pq2_0 b; std::memcpy(&b, w, sizeof b);
+    return pq2_0_dot_f32(&b, a);
+}
 
 // int32 chunk dot through the reference's own pq2_0_dot_q8_1_block: with both
 // scales forced to fp16 1.0 the returned float is exactly (float)sumi

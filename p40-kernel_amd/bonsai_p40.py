@@ -33,6 +33,7 @@ SIGNATURES = {
     "bonsai_p40_repack": [_V, _V, _I64, _I64, _V],
     "bonsai_p40_gemv_repack": [_V, _F32P, _F32P, _I64, _I64, _V],
     "bonsai_p40_fwht": [_F32P, _F32P, _I64, _V],
+    "bonsai_p40_fwht_signs_n": [_F32P, _F32P, _I64, _V],
     "bonsai_p40_rmsnorm": [_F32P, _F32P, _F32P, _I64, _I64, C.c_float, _V],
     "bonsai_p40_gdn_step": [_F32P] * 7 + [C.c_int] * 4 + [_V],
     "bonsai_p40_attn": [_F32P] * 4 + [C.c_int] * 4 + [C.c_float, _V],
@@ -44,8 +45,11 @@ SIGNATURES = {
     "bonsai_p40_gemv_group": [_V, _V, _V, C.c_int, _V, _I64, _V],
     "bonsai_p40_fwht_gemv_group": [_V, _V, _V, C.c_int, _F32P, _F32P, _I64, _V],
     "bonsai_p40_rmsnorm_fwht_gemv_group": [_V, _V, _V, C.c_int, _F32P, _F32P, _F32P, _I64, C.c_float, _V],
+    "bonsai_p40_quantize_pq2_0": [_F32P, _V, _I64, _V],
+    "bonsai_p40_dequantize_pq2_0": [_V, _F32P, _I64, _V],
     "bonsai_p40_chunk_dots": [_V, _V, _V, _I64, _I64, _V],
     "bonsai_p40_stream_read": [_V, _I64, _V, C.c_int, _V],
+    "bonsai_p40_reload_tuning": [],
 }
 
 _lib = None
@@ -123,7 +127,15 @@ def gemv_repack(W, x, y, n_out: int, n_in: int, stream=None) -> None:
 
 
 def fwht(x, signs, n: int, stream=None) -> None:
+    """In-place FWHT-1024 blocks; signs (or None) has 1024 entries reused by
+    every block, as the reference device kernel."""
     _check("bonsai_p40_fwht", call("bonsai_p40_fwht", x, signs, n, stream=stream))
+
+
+def fwht_signs_n(x, signs, n: int, stream=None) -> None:
+    """In-place FWHT-1024 blocks; signs (or None) is a length-n vector, block
+    b using signs[1024 b ..] (the host fwht_blocks form)."""
+    _check("bonsai_p40_fwht_signs_n", call("bonsai_p40_fwht_signs_n", x, signs, n, stream=stream))
 
 
 def rmsnorm(x, w, y, n_rows: int, n: int, eps: float, stream=None) -> None:
@@ -193,9 +205,22 @@ def rmsnorm_fwht_gemv_group(Ws, x, norm_w, signs, ys, n_outs, n_in: int, eps: fl
     _check("bonsai_p40_rmsnorm_fwht_gemv_group", rc)
 
 
+def quantize_pq2_0(x, w, n: int, stream=None) -> None:
+    _check("bonsai_p40_quantize_pq2_0", call("bonsai_p40_quantize_pq2_0", x, w, n, stream=stream))
+
+
+def dequantize_pq2_0(w, y, n: int, stream=None) -> None:
+    _check("bonsai_p40_dequantize_pq2_0", call("bonsai_p40_dequantize_pq2_0", w, y, n, stream=stream))
+
+
 def chunk_dots(W, xq, out, n_out: int, n_in: int, stream=None) -> None:
     _check("bonsai_p40_chunk_dots",
            call("bonsai_p40_chunk_dots", W, xq, out, n_out, n_in, stream=stream))
+
+
+def reload_tuning() -> None:
+    """Re-read the BONSAI_* tuning variables after changing os.environ."""
+    _check("bonsai_p40_reload_tuning", lib().bonsai_p40_reload_tuning())
 
 
 def stream_read(buf, nbytes: int, out, blocks: int, stream=None) -> None:

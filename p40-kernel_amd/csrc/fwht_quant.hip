@@ -40,11 +40,14 @@ enum : int {
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
-// Grid (n/1024, n_tok), 64 threads.  `x` is [n_tok][n].
+// Grid (n/1024, n_tok), 64 threads.  `x` is [n_tok][n].  Block b reads its
+// signs at signs + b * sign_stride: 1024 for a length-n vector (the host
+// form), 0 for one 1024-entry vector reused by every block (the reference
+// device kernel's form).
 template <int MODE>
 __global__ void __launch_bounds__(64)
 rot_quant_kernel(const float * __restrict__ x, const float * __restrict__ signs, float * __restrict__ xout,
-                 uint8_t * __restrict__ q, int n, int n_tok) {
+                 uint8_t * __restrict__ q, int n, int n_tok, int sign_stride) {
     const int l = threadIdx.x;
     const int blk = blockIdx.x;
     const int tok = blockIdx.y;
@@ -56,7 +59,7 @@ rot_quant_kernel(const float * __restrict__ x, const float * __restrict__ signs,
     load16(x + base, v, vec);
     if (MODE & M_SIGNS) {
         float sg[16];
-        load16(signs + (size_t)blk * HBLK + 16 * row, sg, vec);
+        load16(signs + (size_t)blk * sign_stride + 16 * row, sg, vec);
 #pragma unroll
         for (int r = 0; r < 16; ++r) v[r] *= sg[r];
     }
@@ -242,13 +245,13 @@ inline bool al4(const void * p) { return ((uintptr_t)p & 3u) == 0; }
 
 template <int MODE>
 int launch_rot(const float * x, const float * signs, float * xout, void * q,
-               int64_t n, int64_t n_tok, hipStream_t st) {
+               int64_t n, int64_t n_tok, hipStream_t st, int sign_stride = HBLK) {
     dim3 grid((unsigned)(n / HBLK), (unsigned)n_tok);
     const bool vec = al16(x) && al16(signs) && al16(xout);
     const bool sg = signs != nullptr;
 #define PQ2_ROT_LAUNCH(M)                                                                         \
     hipLaunchKernelGGL(rot_quant_kernel<(M)>, grid, dim3(64), 0, st, x, signs, xout,         \
-                       (uint8_t *)q, (int)n, (int)n_tok)
+                       (uint8_t *)q, (int)n, (int)n_tok, sign_stride)
     if (vec && sg) PQ2_ROT_LAUNCH(MODE | M_VEC | M_SIGNS);
     else if (vec) PQ2_ROT_LAUNCH(MODE | M_VEC);
     else if (sg) PQ2_ROT_LAUNCH(MODE | M_SIGNS);
@@ -280,7 +283,15 @@ extern "C" {
 int bonsai_p40_fwht(float * x, const float * signs, int64_t n, bonsai_stream stream) {
     if (n <= 0 || n % HBLK != 0 || x == nullptr) return 1;
     if (n / HBLK > 0x7fffffff) return 1;
-    return launch_rot<M_ROT | M_OUT_F32>(x, signs, x, nullptr, n, 1, (hipStream_t)stream);
+    // the reference device kernel's meaning: signs[0..1023] for every block
+    // (elementwise_p40.cu:23), so no sign past the 1024th is ever read
+    return launch_rot<M_ROT | M_OUT_F32>(x, signs, x, nullptr, n, 1, (hipStream_t)stream, 0);
+}
+
+int bonsai_p40_fwht_signs_n(float * x, const float * signs, int64_t n, bonsai_stream stream) {
+    if (n <= 0 || n % HBLK != 0 || x == nullptr) return 1;
+    if (n / HBLK > 0x7fffffff) return 1;
+    return launch_rot<M_ROT | M_OUT_F32>(x, signs, x, nullptr, n, 1, (hipStream_t)stream, HBLK);
 }
 
 int bonsai_p40_quant_activations(const float * x, void * out, int64_t n, bonsai_stream stream) {

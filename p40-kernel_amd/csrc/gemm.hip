@@ -25,6 +25,7 @@
 //   before the current block is computed.
 // * Small batches (n_tok <= 32) use a 128 x 32 tile (4 waves stacked on rows).
 #include "pq2_device.h"
+#include "host_state.h"
 #include "../../include/bonsai_p40.h"
 
 #include <stdlib.h>
@@ -607,13 +608,10 @@ int launch_small_t(const uint8_t * W, const uint8_t * X, float * Y, int n_out, i
                    hipStream_t st) {
     using C = SkinnyCfg<RT, KS, NT>;
     auto kern = gemm_small_kernel<RT, KS, NT>;
-    static bool attr = false;
-    if (!attr) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS) != hipSuccess)
-            (void)hipGetLastError();   // a refused request must not linger as the launch's error
-        attr = true;
-    }
+    static pq2host::PerDeviceOnce attr;
+    pq2host::once_per_device(attr, [&] {
+        pq2host::set_max_dynamic_lds(reinterpret_cast<const void *>(kern), C::LDS);
+    });
     hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(n_out, C::R)), dim3(64 * KS), C::LDS, st, W, X, Y,
                        n_out, n_tok, nb);
     return (int)hipGetLastError();
@@ -802,13 +800,10 @@ int launch_bd_t(const uint8_t * W, const uint8_t * X, float * Y, int n_out, int 
     using C = SkinnyCfg<RT, KS, NT>;
     constexpr int lds = C::LDS + BdShape<NT>::ZERO;
     auto kern = gemm_bd_kernel<RT, KS, NT>;
-    static bool attr = false;
-    if (!attr) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
-            (void)hipGetLastError();   // a refused request must not linger as the launch's error
-        attr = true;
-    }
+    static pq2host::PerDeviceOnce attr;
+    pq2host::once_per_device(attr, [&] {
+        pq2host::set_max_dynamic_lds(reinterpret_cast<const void *>(kern), lds);
+    });
     hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(n_out, C::R)), dim3(64 * KS), lds, st, W, X, Y, n_out, nb);
     return (int)hipGetLastError();
 }
@@ -863,38 +858,18 @@ void launch_gemm(const uint8_t * W, const uint8_t * X, float * Y, int n_out, int
                        n_out, n_tok, nb);
 }
 
-int env_int_gemm(const char * name, int dflt) {
-    const char * v = getenv(name);
-    return (v && *v) ? atoi(v) : dflt;
-}
+using pq2host::knob;
 
-int gemm_cu_count() {
-    static int v = -1;
-    if (v < 0) {
-        int dev = 0, x = 0;
-        (void)hipGetDevice(&dev);
-        if (hipDeviceGetAttribute(&x, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || x <= 0) {
-            (void)hipGetLastError();
-            x = 256;
-        }
-        v = x;
-    }
-    return v;
-}
+int gemm_cu_count() { return pq2host::device_info().cus; }
 
+// LDS limit of the skinny kernel on the current device (its dynamic-LDS
+// attribute raised to the device maximum once per device)
 int skinny_lds_limit() {
-    static int v = -1;
-    if (v < 0) {
-        int dev = 0;
-        (void)hipGetDevice(&dev);
-        int x = 0;
-        if (hipDeviceGetAttribute(&x, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || x <= 0)
-            x = 64 * 1024;
-        v = x;
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_skinny_kernel),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, x) != hipSuccess)
-            (void)hipGetLastError();   // a refused request must not linger as the launch's error
-    }
+    const int v = pq2host::device_info().max_lds;
+    static pq2host::PerDeviceOnce attr;
+    pq2host::once_per_device(attr, [v] {
+        pq2host::set_max_dynamic_lds(reinterpret_cast<const void *>(gemm_skinny_kernel), v);
+    });
     return v;
 }
 
@@ -1047,10 +1022,13 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
             r.sh = (uint32_t)((a_off + w_align) & 3);
             r.w[0] = *reinterpret_cast<const uint32_t *>(W + aa);
             r.w[1] = *reinterpret_cast<const uint32_t *>(W + aa + 4);
-            // the window may end 2 bytes past W when its last byte is the matrix's
-            // last: then read the dword ending at W's end and shift (flag in sh bit 2)
+            // the window may end past W when its last chunk is the matrix's last.
+            // Shift 2: the code bytes end 2 bytes into the third dword, so read
+            // the dword ending at W's end and shift (flag in sh bit 2).  Shift 0:
+            // the third dword is not used (alignbyte by 0 keeps w[1]), so re-read
+            // the second one.  Every dword read lies in [0, w_bytes).
             const bool tail = aa + 12 > w_bytes;
-            r.w[2] = *reinterpret_cast<const uint32_t *>(W + (tail ? aa + 6 : aa + 8));
+            r.w[2] = *reinterpret_cast<const uint32_t *>(W + (tail ? (r.sh ? aa + 6 : aa + 4) : aa + 8));
             r.sh |= (tail ? 4u : 0u) | (pf_block < nb ? 8u : 0u);
             r.w[3] = (uint32_t)*reinterpret_cast<const uint16_t *>(W + a_off - 2 - 8 * ap);   // block scale
         }
@@ -1237,8 +1215,8 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
     const uint8_t * w = (const uint8_t *)W;
     const uint8_t * x = (const uint8_t *)Xq;
     if (n_tok == 1) return bonsai_p40_gemv(W, Xq, Y, n_out, n_in, stream);   // chunk-major == token-major
-    const int bd_cfg = env_int_gemm("BONSAI_GEMM_BD", -1) < 0 ? bd_choice(nb, n_out, n_tok)
-                                                              : env_int_gemm("BONSAI_GEMM_BD", 0);
+    const int bd_cfg = knob(pq2host::K_GEMM_BD, -1) < 0 ? bd_choice(nb, n_out, n_tok)
+                                                              : knob(pq2host::K_GEMM_BD, 0);
     if (bd_cfg > 0 && n_tok >= 3 && n_tok <= 8 && nb % 2 == 0 && nb >= 16 && ((uintptr_t)W & 3u) == 0 &&
         ((uintptr_t)Xq & 15u) == 0) {
         switch (bd_cfg) {
@@ -1253,10 +1231,10 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
         if (rc >= 0) return rc;
     }
     const size_t skinny_lds = (size_t)4 * 16 * PQ2_BYTES * (nb / 4) + 4096;
-    const int small_sel = env_int_gemm("BONSAI_GEMM_SMALL", 0);   // 0 streamed, 1 previous kernel
+    const int small_sel = knob(pq2host::K_GEMM_SMALL, 0);   // 0 streamed, 1 previous kernel
     if (n_tok <= 16 && small_sel == 0 && nb % 2 == 0 && nb >= 8 && ((uintptr_t)W & 3u) == 0 &&
         ((uintptr_t)Xq & 15u) == 0) {
-        switch (env_int_gemm("BONSAI_GEMM_SMALL_CFG", 0)) {
+        switch (knob(pq2host::K_GEMM_SMALL_CFG, 0)) {
             case 1: return launch_small_nt<1, 4>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
             case 2: return launch_small_nt<2, 4>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
             case 3: return launch_small_nt<4, 4>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
@@ -1277,7 +1255,7 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
                            (int)n_out, (int)n_tok, nb);
         return (int)hipGetLastError();
     }
-    if (env_int_gemm("BONSAI_GEMM_KERNEL", 0) == 0) {
+    if (knob(pq2host::K_GEMM_KERNEL, 0) == 0) {
         // 16 waves (4 per SIMD, 32 x 32 wave tiles) measured 12-22 % faster than
         // 8 waves (2 per SIMD, 64 x 32) on every prefill shape: the latency of
         // the chunk pipeline and the per-block barrier is hidden by more waves.
@@ -1286,7 +1264,7 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
         // M = 256: 61 -> 42 us); past that the extra round costs more than the
         // idle CUs (5120x17408 at M = 512: 200 -> 256 us), so 128.
         const int64_t tiles128 = cdiv(n_out, GF_BM) * cdiv(n_tok, 128);
-        int bn = env_int_gemm("BONSAI_GEMM_F16_BN", 0);
+        int bn = knob(pq2host::K_GEMM_F16_BN, 0);
         if (bn != 64 && bn != 128) bn = 2 * tiles128 <= gemm_cu_count() ? 64 : 128;
         // A last round that only part-fills the CUs (17408 rows at M = 512:
         // 544 tiles = 2 rounds + 32 tiles) costs a whole round.  Where the
@@ -1296,7 +1274,7 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
         const int cus = gemm_cu_count();
         const int64_t ttok = cdiv(n_tok, 128), rounds = tiles128 / cus, rest = tiles128 - rounds * cus;
         if (bn == 128 && rounds >= 1 && rest > 0 && 2 * rest <= cus && (rounds * cus) % ttok == 0 &&
-            env_int_gemm("BONSAI_GEMM_F16_SPLIT", 1) > 0 && env_int_gemm("BONSAI_GEMM_F16_WAVES", 16) != 8) {
+            knob(pq2host::K_GEMM_F16_SPLIT, 1) > 0 && knob(pq2host::K_GEMM_F16_WAVES, 16) != 8) {
             const int64_t rows_main = rounds * cus / ttok * GF_BM;
             const int64_t rows_tail = n_out - rows_main;
             if (rows_tail > 0 && cdiv(rows_tail, GF_BM) * cdiv(n_tok, 64) <= cus) {
@@ -1310,7 +1288,7 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
             }
         }
         const dim3 grid((unsigned)cdiv(n_out, GF_BM), (unsigned)cdiv(n_tok, bn));
-        if (env_int_gemm("BONSAI_GEMM_F16_WAVES", 16) == 8)
+        if (knob(pq2host::K_GEMM_F16_WAVES, 16) == 8)
             hipLaunchKernelGGL((gemm_f16_kernel<2, 4, 4, 2>), dim3(grid.x, (unsigned)cdiv(n_tok, 128)), dim3(512),
                                0, st, w, x, Y, (int)n_out, (int)n_tok, nb);
         else if (bn == 64)

@@ -28,6 +28,7 @@
 //   row_half_mirror, row_mirror, row_bcast15/31) and lane 63 stores y.
 // Any other shape or alignment takes a simple wave-per-row kernel.
 #include "fwht_device.h"
+#include "host_state.h"
 #include "../../include/bonsai_p40.h"
 
 #include <stdlib.h>
@@ -777,37 +778,20 @@ gemv_rowwave_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__
     }
 }
 
-int env_int(const char * name, int dflt) {
-    const char * s = getenv(name);
-    return (s && *s) ? atoi(s) : dflt;
-}
+using pq2host::knob;
 
-int max_lds_per_block() {
-    static int v = -1;
-    if (v < 0) {
-        int dev = 0;
-        (void)hipGetDevice(&dev);
-        int x = 0;
-        if (hipDeviceGetAttribute(&x, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || x <= 0)
-            x = 64 * 1024;
-        v = x;
-    }
-    return v;
-}
+int max_lds_per_block() { return pq2host::device_info().max_lds; }
 
 template <int G, int NPL, bool DUMP>
 int launch_stream_t(const uint8_t * W, const uint8_t * xq, float * y, int32_t * dump, int n_out,
                     const StreamGeom & g, hipStream_t st) {
     auto kern = gemv_stream_kernel<G, NPL, DUMP>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, max_lds_per_block()) != hipSuccess)
-            (void)hipGetLastError();   // a refused request must not linger as the launch's error
-        attr_set = true;
-    }
+    static pq2host::PerDeviceOnce attr;
+    pq2host::once_per_device(attr, [&] {
+        pq2host::set_max_dynamic_lds(reinterpret_cast<const void *>(kern), max_lds_per_block());
+    });
     const int n_units = (n_out + G - 1) / G;
-    int upw = env_int("BONSAI_GEMV_UNITS_PER_WAVE", 0);
+    int upw = knob(pq2host::K_GEMV_UNITS_PER_WAVE, 0);
     if (upw <= 0) {
         const int target_waves = 256 * 12;
         upw = (n_units + target_waves - 1) / target_waves;
@@ -834,18 +818,7 @@ int launch_stream_g(const uint8_t * W, const uint8_t * xq, float * y, int32_t * 
     }
 }
 
-int cu_count() {
-    static int v = -1;
-    if (v < 0) {
-        int dev = 0;
-        (void)hipGetDevice(&dev);
-        int x = 0;
-        if (hipDeviceGetAttribute(&x, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || x <= 0)
-            x = 256;
-        v = x;
-    }
-    return v;
-}
+int cu_count() { return pq2host::device_info().cus; }
 
 // Workgroups per CU for the decode GEMV, from sweeps on MI355X (HIP-graph
 // replay, weights streamed from HBM): rows of <= 48 blocks want 3 workgroups
@@ -906,7 +879,7 @@ int launch_nb_t(MatGroup mg, int n_mat, const void * xin, const float * signs, i
     }
     // groups of 2^xl consecutive units per XCD: 4 units cut HBM fetch by 3.4 % and time by
     // 3-5 % on the model's shapes against plain numbering; 8 units measured another ~1 %
-    int xl = env_int("BONSAI_GEMV_XCD_LOG2M", 3);
+    int xl = knob(pq2host::K_GEMV_XCD_LOG2M, 3);
     if (xl < 0 || xl > 3 || blocks % 8 != 0) xl = 0;
     while (xl > 0 && ((blocks / 8) * WAVES) % (1 << xl) != 0) --xl;
     if constexpr (OVL) {
@@ -948,7 +921,7 @@ template <int NB, bool DUMP>
 int launch_nb(const MatGroup & mg, int n_mat, const uint8_t * xq, int32_t * dump, hipStream_t st) {
     // 4-wave workgroups with two unit buffers per wave measured best at every
     // model width (deeper rings queue more bytes ahead of the activation)
-    int per_cu = env_int("BONSAI_GEMV_WG_PER_CU", 0);
+    int per_cu = knob(pq2host::K_GEMV_WG_PER_CU, 0);
     if (per_cu <= 0) {
         per_cu = default_wg_per_cu(NB, group_weight_bytes(mg, n_mat, NB));
         // a matrix below 16 MB whose units fill one 4-wave workgroup per CU
@@ -1150,7 +1123,7 @@ int launch_mfma4(const uint8_t * W, const uint8_t * X, float * Y, int n_out, int
     constexpr int lds = mfma4_lds_bytes<NB, NTG, WAVES>();
     static_assert(lds <= LDS_PER_CU, "workgroup LDS");
     const int n_units = (n_out + 3) / 4;
-    int per_cu = env_int("BONSAI_MFMA4_WG_PER_CU", LDS_PER_CU / lds);
+    int per_cu = knob(pq2host::K_MFMA4_WG_PER_CU, LDS_PER_CU / lds);
     if (per_cu > LDS_PER_CU / lds) per_cu = LDS_PER_CU / lds;
     if (per_cu < 1) per_cu = 1;
     int blocks = per_cu * cu_count();
@@ -1170,7 +1143,7 @@ int launch_mfma4(const uint8_t * W, const uint8_t * X, float * Y, int n_out, int
 // workgroups) below 4096 rows -- measured on MI355X.
 template <int NB>
 int launch_mfma4_nt(const uint8_t * W, const uint8_t * X, float * Y, int n_out, int n_tok, hipStream_t st) {
-    const int waves = env_int("BONSAI_MFMA4_WAVES", n_out >= 4096 ? 8 : 4);
+    const int waves = knob(pq2host::K_MFMA4_WAVES, n_out >= 4096 ? 8 : 4);
     if (waves == 4) return launch_mfma4<NB, 1, 4>(W, X, Y, n_out, n_tok, st);
     return launch_mfma4<NB, 1, 8>(W, X, Y, n_out, n_tok, st);
 }
@@ -1188,7 +1161,7 @@ int launch_nb_small(const uint8_t * W, const uint8_t * X, float * Y, int n_out, 
         return -1;
     } else {
         MatGroup mg = single_group(W, Y, n_out);
-        int per_cu = env_int("BONSAI_GEMV_WG_PER_CU", 0);
+        int per_cu = knob(pq2host::K_GEMV_WG_PER_CU, 0);
         if (per_cu <= 0) per_cu = default_wg_per_cu(NB, (int64_t)n_out * PQ2_BYTES * NB);
         return launch_nb_t<NB, 2, 4, false, 0, NT>(mg, 1, X, nullptr, nullptr, per_cu, st, n_tok);
     }
@@ -1211,14 +1184,14 @@ int launch_nb_small_nt(const uint8_t * W, const uint8_t * X, float * Y, int n_ou
 // with D = 2 or D = 1.  Returns -1 when no shape fits the LDS of a workgroup.
 template <int NB, int ROT, bool RP = false, bool RMS = false>
 int launch_nb_rot(const MatGroup & mg, int n_mat, const float * x, const float * signs, hipStream_t st) {
-    const int waves = env_int("BONSAI_FGEMV_WAVES", 8);
-    int per_cu = env_int("BONSAI_GEMV_WG_PER_CU", 0);
+    const int waves = knob(pq2host::K_FGEMV_WAVES, 8);
+    int per_cu = knob(pq2host::K_GEMV_WG_PER_CU, 0);
     if (per_cu <= 0) per_cu = 1;
     if constexpr (nb_lds_bytes<NB, 2, 8, ROT, 1, RMS>() <= LDS_PER_CU) {
         if (waves == 8) return launch_nb_t<NB, 2, 8, false, ROT, 1, RP, RMS>(mg, n_mat, x, signs, nullptr, per_cu, st);
     } else if constexpr (ROT == 1 && !RP && !RMS && nb_lds_bytes<NB, 2, 8, 1, 1, false, true>() <= LDS_PER_CU) {
         // the separate stage does not fit beside an 8-wave ring: stage in the ring
-        if (waves == 8 && env_int("BONSAI_FGEMV_OVL", 1) == 1)
+        if (waves == 8 && knob(pq2host::K_FGEMV_OVL, 1) == 1)
             return launch_nb_t<NB, 2, 8, false, 1, 1, false, false, true>(mg, n_mat, x, signs, nullptr, per_cu, st);
     }
     if constexpr (nb_lds_bytes<NB, 2, 4, ROT, 1, RMS>() <= LDS_PER_CU)
@@ -1313,7 +1286,7 @@ int fwht_gemv_group_dispatch(const MatGroup & mg, int n_mat, const float * x, co
                              int64_t n_in, hipStream_t st) {
     const bool al = group_w_aligned(mg, n_mat) && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)signs & 15u) == 0 &&
                     ((uintptr_t)mg.norm_w & 15u) == 0;
-    if (al && env_int("BONSAI_GEMV_KERNEL", 0) == 0) {
+    if (al && knob(pq2host::K_GEMV_KERNEL, 0) == 0) {
         int rc = -1;
         if (mg.norm_w != nullptr) {
             // RMSNorm on the widths a layer input has (the model's 5120 and 6144,
@@ -1341,16 +1314,12 @@ int fwht_gemv_group_dispatch(const MatGroup & mg, int n_mat, const float * x, co
     }
     const size_t lds = rot_generic_lds(n_in);
     if (lds > (size_t)max_lds_per_block()) return 1;
-    static bool attr_set = false;
-    if (!attr_set) {
-        // the kernel's static LDS (its fp64 partial sums) comes off the maximum;
-        // a refused request must not linger as the launch's error
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_rot_generic_kernel),
-                                hipFuncAttributeMaxDynamicSharedMemorySize,
-                                max_lds_per_block() - 1024) != hipSuccess)
-            (void)hipGetLastError();
-        attr_set = true;
-    }
+    // the kernel's static LDS (its fp64 partial sums) comes off the maximum
+    static pq2host::PerDeviceOnce attr;
+    pq2host::once_per_device(attr, [] {
+        pq2host::set_max_dynamic_lds(reinterpret_cast<const void *>(gemv_rot_generic_kernel),
+                                     max_lds_per_block() - 1024);
+    });
     if (lds > (size_t)max_lds_per_block() - 1024) return 1;
     const bool vec = ((uintptr_t)x & 15u) == 0 && ((uintptr_t)signs & 15u) == 0 &&
                      ((uintptr_t)mg.norm_w & 15u) == 0;
@@ -1389,7 +1358,7 @@ template <bool DUMP>
 int gemv_group_dispatch(const MatGroup & mg, int n_mat, const void * xq, int32_t * dump, int64_t n_in,
                         hipStream_t st) {
     const uint8_t * x = static_cast<const uint8_t *>(xq);
-    const int kernel_sel = env_int("BONSAI_GEMV_KERNEL", 0);   // 0 auto, 1 stream, 2 generic
+    const int kernel_sel = knob(pq2host::K_GEMV_KERNEL, 0);   // 0 auto, 1 stream, 2 generic
     if (group_w_aligned(mg, n_mat) && ((uintptr_t)x & 15u) == 0 && kernel_sel == 0) {
         switch (n_in / QK_PQ2) {
             case 8: return launch_nb<8, DUMP>(mg, n_mat, x, dump, st);
@@ -1446,12 +1415,12 @@ int gemv_small_batch(const void * W, const void * Xq, float * Y, int64_t n_out, 
                      int64_t n_tok, bonsai_stream stream) {
     if (n_tok < 2 || n_tok > 4 || n_out <= 0 || n_out > 0x3fffffff) return -1;
     if (((uintptr_t)W & 15u) != 0 || ((uintptr_t)Xq & 15u) != 0) return -1;
-    if (n_tok > env_int("BONSAI_GEMM_SMALL_GEMV", 4)) return -1;
+    if (n_tok > knob(pq2host::K_GEMM_SMALL_GEMV, 4)) return -1;
     const uint8_t * w = static_cast<const uint8_t *>(W);
     const uint8_t * x = static_cast<const uint8_t *>(Xq);
     hipStream_t st = (hipStream_t)stream;
     const int nb = (int)(n_in / QK_PQ2);
-    if (n_tok >= env_int("BONSAI_MFMA4_MIN_TOK", 3) && (nb == 8 || nb == 40 || nb == 48)) {
+    if (n_tok >= knob(pq2host::K_MFMA4_MIN_TOK, 3) && (nb == 8 || nb == 40 || nb == 48)) {
         switch (nb) {
             case 8: return launch_mfma4_nt<8>(w, x, Y, (int)n_out, (int)n_tok, st);
             case 40: return launch_mfma4_nt<40>(w, x, Y, (int)n_out, (int)n_tok, st);
@@ -1479,7 +1448,7 @@ int gemv_repack_streaming(const void * W, const float * x, float * y, int64_t n_
                           bonsai_stream stream) {
     if (n_out <= 0 || n_out > 0x3fffffff) return -1;
     if (((uintptr_t)W & 15u) != 0 || ((uintptr_t)x & 15u) != 0) return -1;
-    if (env_int("BONSAI_GEMV_KERNEL", 0) != 0) return -1;
+    if (knob(pq2host::K_GEMV_KERNEL, 0) != 0) return -1;
     const MatGroup mg = single_group(W, y, n_out);
     hipStream_t st = (hipStream_t)stream;
     switch (n_in / QK_PQ2) {

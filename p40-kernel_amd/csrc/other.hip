@@ -3,8 +3,11 @@
 //   * bonsai_p40_rmsnorm: per-row RMSNorm, y = x * (1/sqrt(mean(x^2)+eps)) * w
 //     (src/ops.h:13-22; the reference device kernel is elementwise_p40.cu:48-88);
 //   * bonsai_p40_gdn_step / bonsai_p40_attn: outside this library's scope,
-//     they return 2 without touching memory.
+//     they return 2 without touching memory;
+// plus bonsai_p40_reload_tuning, which re-reads the library's BONSAI_* tuning
+// variables (read once per process otherwise).
 #include "pq2_device.h"
+#include "host_state.h"
 #include "../../include/bonsai_p40.h"
 
 using namespace pq2;
@@ -52,3 +55,8 @@ int bonsai_p40_attn(const float *, const float *, const float *, float *, int, i
 }
 
 }  // extern "C"
+
+extern "C" int bonsai_p40_reload_tuning(void) {
+    pq2host::reload_knobs();
+    return 0;
+}

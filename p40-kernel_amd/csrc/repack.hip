@@ -14,6 +14,7 @@
 // with one dwordx2 load, and the block scales of consecutive units are
 // consecutive fp16 values.
 #include "pq2_device.h"
+#include "host_state.h"
 #include "../../include/bonsai_p40.h"
 
 using namespace pq2;
@@ -130,18 +131,7 @@ gemv_repack_kernel(const uint8_t * __restrict__ W, const float * __restrict__ x,
     }
 }
 
-int lds_limit() {
-    static int v = -1;
-    if (v < 0) {
-        int dev = 0;
-        (void)hipGetDevice(&dev);
-        int x = 0;
-        if (hipDeviceGetAttribute(&x, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || x <= 0)
-            x = 64 * 1024;
-        v = x;
-    }
-    return v;
-}
+int lds_limit() { return pq2host::device_info().max_lds; }
 
 }  // namespace
 
@@ -181,13 +171,10 @@ int bonsai_p40_gemv_repack(const void * W, const float * x, float * y, int64_t n
     if (rc >= 0) return rc;
     const size_t lds = (size_t)nb * 4 * 40;
     if (lds > (size_t)lds_limit()) return 1;
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_repack_kernel),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds_limit()) != hipSuccess)
-            (void)hipGetLastError();   // a refused request must not linger as the launch's error
-        attr_set = true;
-    }
+    static pq2host::PerDeviceOnce attr;
+    pq2host::once_per_device(attr, [] {
+        pq2host::set_max_dynamic_lds(reinterpret_cast<const void *>(gemv_repack_kernel), lds_limit());
+    });
     int64_t blocks = (n_out + RP_WAVES - 1) / RP_WAVES;
     if (blocks > 256 * 4) blocks = 256 * 4;
     hipLaunchKernelGGL(gemv_repack_kernel, dim3((unsigned)blocks), dim3(RP_THREADS), lds,

@@ -1,4 +1,4 @@
-"""Writes the golden fixtures F1-F8 from the reference's own host code.
+"""Writes the golden fixtures F1-F9 from the reference's own host code.
 
 The vectors come from oracle/_ref/libbonsai_ref.so, i.e. the reference
 headers src/pq2_0.h, src/fwht.h, src/pq2_0_repack.h and src/ops.h compiled
@@ -86,6 +86,26 @@ def tie_chunk():
     return x
 
 
+def pq2_special_blocks():
+    """Blocks for the ternary quantiser's edge cases (src/pq2_0.h:74-90)."""
+    blocks = []
+    b = np.zeros(128, np.float32)            # all zero: d = 0, id = 0, every code 1
+    blocks.append(b)
+    b = np.zeros(128, np.float32)            # x * id exactly +-0.5: lroundf goes away from zero
+    b[0] = 2.0
+    b[1:9] = [1.0, -1.0, 1.0, -1.0, 0.5, -0.5, 1.5, -1.5]
+    b[9:] = np.linspace(-2.0, 2.0, 119).astype(np.float32)
+    blocks.append(b)
+    b = np.linspace(-1.0, 1.0, 128).astype(np.float32)
+    b[5] = 1.0 + 2.0 ** -11                  # amax an exact fp16 tie (1 and 1 + 2^-10): ties away
+    blocks.append(b)
+    blocks.append(np.linspace(-1e-6, 3e-6, 128).astype(np.float32))    # subnormal fp16 scale
+    blocks.append(np.linspace(-7e4, 1e5, 128).astype(np.float32))      # scale overflows fp16
+    b = -np.abs(np.linspace(0.1, 3.0, 128)).astype(np.float32)        # all negative
+    blocks.append(b)
+    return np.concatenate(blocks)
+
+
 def main():
     R = O.ref()
     if R is None:
@@ -170,6 +190,21 @@ def main():
         fx[tag + "_x"], fx[tag + "_w"], fx[tag + "_y"] = x, w, y
         fx[tag + "_eps"] = np.float32(eps)
         fx[tag + "_yq"] = ref_q8(R, ref_fwht(R, y), True)
+
+    # F9: reference ternary quantiser, dequantiser and float block dot
+    #     (src/pq2_0.h:62-90, 134-142)
+    xs = np.concatenate([O.gen_normal(115, 8 * 1024, 0.02), pq2_special_blocks()])
+    w9 = np.empty(xs.size // 128 * 34, np.uint8)
+    R.ref_quantize_pq2_0(p(xs, O._f32p), p(w9, O._u8p), xs.size)
+    fx["f9_x"], fx["f9_w"] = xs, w9
+    wd = np.concatenate([w9, fx["f4_5120_W"][:34 * 40]])       # plus code-3-rich rows
+    yd = np.empty(wd.size // 34 * 128, np.float32)
+    R.ref_dequantize_pq2_0(p(wd, O._u8p), p(yd, O._f32p), yd.size)
+    fx["f9_wd"], fx["f9_deq"] = wd, yd
+    a9 = O.gen_normal(116, yd.size) * 3
+    fx["f9_a"] = a9
+    fx["f9_dot"] = np.array([R.ref_pq2_0_dot_f32(p(wd[34 * i:], O._u8p), p(a9[128 * i:], O._f32p))
+                             for i in range(wd.size // 34)], np.float32)
 
     np.savez_compressed(OUT, **fx)
     print(f"wrote {OUT}: {os.path.getsize(OUT)} bytes, {len(fx)} arrays")

@@ -216,3 +216,54 @@ def test_block_diagonal_small_batch_emulation(NT):
     ref = O.gemm(W, X, n_out, n_in, NT)
     scale = float(np.max(np.abs(ref)))
     assert float(np.max(np.abs(y - ref))) <= 1e-5 * scale
+
+
+# ------------------------------------------------------------------------
+# Address math of the prefill GEMM's weight staging (gemm_f16_kernel,
+# p40-kernel_amd/csrc/gemm.hip, `prefetch`): per (row, chunk ap, block) the
+# kernel reads a dword-aligned window of three dwords over the chunk's 8 code
+# bytes plus the 2-byte block scale, with W at any 2-byte alignment.  Restated
+# here on the CPU: every byte read must lie in [0, w_bytes) -- an exact-size
+# allocation can end at an unmapped page -- and the realigned words must be
+# the chunk's code bytes.
+def _alignbyte(hi, lo, s):
+    return ((((hi.astype(np.uint64) << np.uint64(32)) | lo.astype(np.uint64)) >> (8 * s).astype(np.uint64))
+            & np.uint64(0xffffffff)).astype(np.uint32)
+
+
+@pytest.mark.parametrize("w_align", [0, 2])
+@pytest.mark.parametrize("n_out,nb", [(17408, 40), (5120, 136), (6144, 40), (1024, 40),
+                                      (129, 3), (200, 5), (64, 8), (7, 1)])
+def test_gemm_f16_weight_window_stays_in_w(n_out, nb, w_align):
+    rs = 34 * nb
+    w_bytes = rs * n_out
+    rows = np.arange(n_out, dtype=np.int64)[:, None, None]
+    blk = np.arange(nb, dtype=np.int64)[None, :, None]
+    ap = np.arange(4, dtype=np.int64)[None, None, :]
+    a_off = rows * rs + 34 * blk + 2 + 8 * ap
+    aa = ((a_off + w_align) & ~3) - w_align
+    sh = (a_off + w_align) & 3
+    tail = aa + 12 > w_bytes
+    third = np.where(tail, np.where(sh != 0, aa + 6, aa + 4), aa + 8)
+    scale = a_off - 2 - 8 * ap
+    lo = np.minimum(np.minimum(aa, third), scale).min()
+    hi = max((aa + 8).max(), (third + 4).max(), (scale + 2).max())
+    assert lo >= 0 and hi <= w_bytes, (lo, hi, w_bytes)
+    assert set(np.unique(sh)) <= {0, 2}
+    # data: the realigned words are the chunk's 8 code bytes (last rows only)
+    rng = np.random.default_rng(nb)
+    buf = rng.integers(0, 256, w_bytes + w_align + 8, dtype=np.uint8)
+    last = slice(max(0, n_out - 3), n_out)
+    A, S, T, TL = (v[last].ravel() for v in (aa, sh, third, np.broadcast_to(tail, aa.shape)))
+    O_ = a_off[last].ravel()
+    def dword(at):
+        idx = w_align + at[:, None] + np.arange(4)
+        return (buf[idx].astype(np.uint32) << (8 * np.arange(4, dtype=np.uint32))).sum(axis=1).astype(np.uint32)
+    w0, w1, w2 = dword(A), dword(A + 4), dword(T)
+    a2 = np.where(TL, w2 >> np.uint32(16), w2)
+    cw0 = _alignbyte(w1, w0, S)
+    cw1 = _alignbyte(a2, w1, S)
+    want0 = dword(O_)
+    want1 = dword(O_ + 4)
+    assert np.array_equal(cw0, want0)
+    assert np.array_equal(cw1, want1)

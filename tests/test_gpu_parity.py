@@ -68,19 +68,32 @@ def test_fwht_fixture_bits(golden):
     B.fwht(x, None, 2048)
     assert np.array_equal(bits(host(x)), bits(golden["f3_out"]))
     x = dev(golden["f3_in"])
-    B.fwht(x, dev(golden["f3_signs"]), 2048)
+    B.fwht_signs_n(x, None, 2048)
+    assert np.array_equal(bits(host(x)), bits(golden["f3_out"]))
+    x = dev(golden["f3_in"])
+    B.fwht_signs_n(x, dev(golden["f3_signs"]), 2048)
     assert np.array_equal(bits(host(x)), bits(golden["f3_out_signed"]))
 
 
 @pytest.mark.parametrize("n,offset", [(5120, 0), (17408, 0), (17408, 1), (1024, 3)])
 def test_fwht_seeded_bits(n, offset):
+    """Both sign meanings: bonsai_p40_fwht reuses signs[0..1023] for every
+    block (the reference device kernel, elementwise_p40.cu:23) and equals the
+    host fwht_blocks with that vector tiled; bonsai_p40_fwht_signs_n reads a
+    length-n vector (src/fwht.h:38-42).  The 1024-entry buffer is followed by
+    NaN guards, which a read past its end would carry into the result."""
     case(f"fwht n={n} float offset={offset}")
     x = O.gen_normal(300 + n, n)
     s = np.where(O.gen_normal(301 + n, n) > 0, 1.0, -1.0).astype(np.float32)
     buf = torch.zeros(n + 8, dtype=torch.float32, device="cuda")
     buf[offset:offset + n] = dev(x)
-    B.fwht(buf.data_ptr() + 4 * offset, dev(s), n)
+    B.fwht_signs_n(buf.data_ptr() + 4 * offset, dev(s), n)
     assert np.array_equal(bits(host(buf)[offset:offset + n]), bits(O.fwht(x, s)))
+    s1 = torch.full((1024 + 64,), float("nan"), dtype=torch.float32, device="cuda")
+    s1[:1024] = dev(s[:1024])
+    buf[offset:offset + n] = dev(x)
+    B.fwht(buf.data_ptr() + 4 * offset, s1, n)
+    assert np.array_equal(bits(host(buf)[offset:offset + n]), bits(O.fwht(x, np.tile(s[:1024], n // 1024))))
 
 
 # ------------------------------------------------------------- quantisers
@@ -211,7 +224,7 @@ def test_gemv_matches_oracle(n_out, n_in, w_offset):
 
 
 @pytest.mark.parametrize("n_out,n_in", [(17408, 5120), (5120, 17408), (6144, 5120), (1024, 5120),
-                                        (5120, 6144), (17407, 5120)])
+                                        (5120, 6144), (17407, 5120), (5120, 5120)])
 def test_gemv_model_shapes(n_out, n_in):
     case(f"gemv model shape {n_out}x{n_in}")
     W, xq = make(n_out, n_in, 900 + n_in)
@@ -478,8 +491,13 @@ def test_gemm_matches_oracle(n_out, n_in, n_tok):
     assert normwise(host(Y), O.gemm(W, Xq, n_out, n_in, n_tok, nthreads=16)) <= TOL
 
 
-@pytest.mark.parametrize("n_out,n_in,n_tok", [(17408, 5120, 512), (5120, 17408, 512)])
+@pytest.mark.parametrize("n_out,n_in,n_tok", [(17408, 5120, 512), (5120, 17408, 512),
+                                              (17408, 5120, 2048), (5120, 17408, 2048)])
 def test_gemm_prefill_shapes_row_sample(n_out, n_in, n_tok):
+    """Config 4: both prefill shapes at M = 512 and 2048 against the oracle
+    on the first and last rows and on rows either side of the split launch
+    (at M = 2048 the rows of the full 128-token-tile rounds and the rest run
+    as two launches)."""
     case(f"gemm prefill {n_out}x{n_in}x{n_tok} (oracle on a row sample)")
     W = O.gen_weights(1200 + n_in, n_out, n_in)
     X = np.stack([O.fwht(O.gen_normal(1201 + t, n_in)) for t in range(n_tok)])
@@ -488,7 +506,8 @@ def test_gemm_prefill_shapes_row_sample(n_out, n_in, n_tok):
     B.gemm(dev(W), dev(Xq), Y, n_out, n_in, n_tok)
     got = host(Y)
     assert np.all(np.isfinite(got))
-    rows = np.r_[0:64, n_out - 64:n_out]
+    cut = 16384 if n_out == 17408 else 4096
+    rows = np.r_[0:64, cut - 32:cut + 32, n_out - 64:n_out]
     rb = n_in // 128 * 34
     Ws = np.concatenate([W[r * rb:(r + 1) * rb] for r in rows])
     ref = O.gemm(Ws, Xq, rows.size, n_in, n_tok, nthreads=16)
@@ -499,14 +518,14 @@ def test_gemm_prefill_shapes_row_sample(n_out, n_in, n_tok):
     (17408, 5120, 2), (6144, 5120, 3), (1025, 5120, 4), (5120, 6144, 2), (77, 6144, 4),
     (333, 1024, 3), (64, 10240, 2), (31, 12288, 2), (17407, 5120, 2), (5120, 17408, 2),
     (301, 17408, 3), (100, 17408, 4), (257, 12288, 4), (5120, 17408, 4)])
-def test_gemm_small_batch_streaming(n_out, n_in, n_tok, monkeypatch):
+def test_gemm_small_batch_streaming(n_out, n_in, n_tok, knobs):
     """With the block-diagonal kernel switched off: 2 tokens run on the
     streaming GEMV kernel with per-token planes (3 on the widths without a
     4x4x4 kernel), 3..4 on the 4x4x4 MFMA kernel (4 on the other widths on
     the 16x16 MFMA kernel): against the oracle, and against one GEMV per
     token (bit-identical for 2 tokens, where the unit shape and the
     arithmetic are the GEMV's)."""
-    monkeypatch.setenv("BONSAI_GEMM_BD", "0")
+    knobs.set("BONSAI_GEMM_BD", "0")
     case(f"gemm small batch {n_out}x{n_in}x{n_tok}")
     W = O.gen_weights(1400 + n_out + n_tok, n_out, n_in)
     X = np.stack([O.fwht(O.gen_normal(1401 + t + n_in, n_in)) for t in range(n_tok)])
@@ -530,11 +549,11 @@ def test_gemm_small_batch_streaming(n_out, n_in, n_tok, monkeypatch):
 @pytest.mark.parametrize("n_out,n_in,n_tok", [
     (17408, 5120, 4), (17408, 5120, 3), (6144, 5120, 4), (5121, 6144, 3), (33, 1024, 4),
     (17407, 5120, 4), (1026, 6144, 4), (7, 5120, 3), (4095, 5120, 4), (4096, 5120, 3)])
-def test_gemm_small_batch_mfma4(n_out, n_in, n_tok, monkeypatch):
+def test_gemm_small_batch_mfma4(n_out, n_in, n_tok, knobs):
     """3..4 tokens on the 4x4x4 MFMA streaming kernel (4- and 8-wave
     workgroups either side of 4096 rows; the block-diagonal kernel switched
     off): against the oracle and against one GEMV per token."""
-    monkeypatch.setenv("BONSAI_GEMM_BD", "0")
+    knobs.set("BONSAI_GEMM_BD", "0")
     case(f"gemm small batch (mfma4) {n_out}x{n_in}x{n_tok}")
     W = O.gen_weights(1600 + n_out + n_tok, n_out, n_in)
     X = np.stack([O.fwht(O.gen_normal(1601 + t + n_in, n_in)) for t in range(n_tok)])
@@ -554,15 +573,16 @@ def test_gemm_small_batch_mfma4(n_out, n_in, n_tok, monkeypatch):
 @pytest.mark.parametrize("cfg", ["auto", "1", "2", "3", "4"])
 @pytest.mark.parametrize("n_out,n_in,n_tok", [
     (17408, 5120, 8), (5120, 17408, 4), (6144, 5120, 5), (1000, 6144, 6), (77, 2048, 7),
-    (33, 17408, 3), (5121, 12288, 8), (17, 10240, 4), (17408, 5120, 3), (5120, 6144, 8)])
-def test_gemm_small_batch_block_diagonal(n_out, n_in, n_tok, cfg, monkeypatch):
+    (33, 17408, 3), (5121, 12288, 8), (17, 10240, 4), (17408, 5120, 3), (5120, 6144, 8),
+    (5120, 17408, 8)])
+def test_gemm_small_batch_block_diagonal(n_out, n_in, n_tok, cfg, knobs):
     """3..8 tokens on the block-diagonal 16x16x64 MFMA kernel in each of its
     workgroup shapes (16 or 32 rows, K split 4 or 8 ways) and through the
     default choice: against the oracle and against one GEMV per token."""
     if cfg == "auto":
-        monkeypatch.delenv("BONSAI_GEMM_BD", raising=False)
+        knobs.unset("BONSAI_GEMM_BD")
     else:
-        monkeypatch.setenv("BONSAI_GEMM_BD", cfg)
+        knobs.set("BONSAI_GEMM_BD", cfg)
     case(f"gemm small batch (block-diagonal cfg {cfg}) {n_out}x{n_in}x{n_tok}")
     W = O.gen_weights(1900 + n_out + n_tok, n_out, n_in)
     X = np.stack([O.fwht(O.gen_normal(1901 + t + n_in, n_in)) for t in range(n_tok)])
@@ -581,19 +601,19 @@ def test_gemm_small_batch_block_diagonal(n_out, n_in, n_tok, cfg, monkeypatch):
 
 @pytest.mark.parametrize("xl", ["0", "1", "2", "3"])
 @pytest.mark.parametrize("n_out,n_in", [(17408, 5120), (5120, 17408), (6144, 5120), (1000, 5120)])
-def test_gemv_xcd_unit_numbering(n_out, n_in, xl, monkeypatch):
+def test_gemv_xcd_unit_numbering(n_out, n_in, xl, knobs):
     """Every XCD grouping of the unit numbering (2^xl consecutive units per
     XCD) covers each unit once: against the oracle and bit-identical to the
     plain numbering (the unit shape and the arithmetic do not change)."""
     case(f"gemv {n_out}x{n_in} XCD group 2^{xl}")
     W, xq = make(n_out, n_in, 3100 + n_out + n_in)
     Wd, xd = dev(W), dev(xq)
-    monkeypatch.setenv("BONSAI_GEMV_XCD_LOG2M", xl)
+    knobs.set("BONSAI_GEMV_XCD_LOG2M", xl)
     y = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
     B.gemv(Wd, xd, y, n_out, n_in)
     got = host(y)
     assert normwise(got, O.gemv(W, xq, n_out, n_in, nthreads=16)) <= TOL
-    monkeypatch.setenv("BONSAI_GEMV_XCD_LOG2M", "0")
+    knobs.set("BONSAI_GEMV_XCD_LOG2M", "0")
     y0 = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
     B.gemv(Wd, xd, y0, n_out, n_in)
     np.testing.assert_array_equal(bits(got), bits(host(y0)))
@@ -619,12 +639,12 @@ def test_gemm_subnormal_and_zero_block_scales():
 
 
 @pytest.mark.parametrize("waves", ["16", "8"])
-def test_gemm_large_block_scales_with_code3(waves, monkeypatch):
+def test_gemm_large_block_scales_with_code3(waves, knobs):
     """Blocks whose fp16 scale has |d| >= 32768 and that hold code 3 (value
     2d, past the fp16 range): the prefill kernel stages d / 2 for them and
     doubles their chunk sums; both workgroup shapes, and the GEMV on the same
     weights."""
-    monkeypatch.setenv("BONSAI_GEMM_F16_WAVES", waves)
+    knobs.set("BONSAI_GEMM_F16_WAVES", waves)
     case(f"gemm 200x2048x64 with |d| >= 32768 and code 3 ({waves} waves)")
     n_out, n_in, n_tok = 200, 2048, 64
     W = O.gen_weights(1700, n_out, n_in).copy()
@@ -654,10 +674,10 @@ def test_gemm_large_block_scales_with_code3(waves, monkeypatch):
 
 @pytest.mark.parametrize("bn", ["64", "128"])
 @pytest.mark.parametrize("n_out,n_in,n_tok", [(1000, 5120, 200), (300, 6144, 77), (129, 1024, 130)])
-def test_gemm_token_tile(bn, n_out, n_in, n_tok, monkeypatch):
+def test_gemm_token_tile(bn, n_out, n_in, n_tok, knobs):
     """Both token tiles of the prefill kernel on ragged shapes (partial row
     and token tiles), against the oracle."""
-    monkeypatch.setenv("BONSAI_GEMM_F16_BN", bn)
+    knobs.set("BONSAI_GEMM_F16_BN", bn)
     case(f"gemm {n_out}x{n_in}x{n_tok} token tile {bn}")
     W = O.gen_weights(2800 + n_out, n_out, n_in)
     X = O.gen_normal(2801 + n_tok, n_tok * n_in).reshape(n_tok, n_in)
@@ -670,7 +690,7 @@ def test_gemm_token_tile(bn, n_out, n_in, n_tok, monkeypatch):
 
 
 @pytest.mark.parametrize("n_out,n_in,n_tok", [(17408, 5120, 512), (5120, 17408, 1024), (17408, 5120, 300)])
-def test_gemm_split_last_round(n_out, n_in, n_tok, monkeypatch):
+def test_gemm_split_last_round(n_out, n_in, n_tok, knobs):
     """Where the 128-token tiles leave a part-filled last round, the rows of
     the full rounds and the remaining rows run as two launches (128- and
     64-token tiles): y is bit-identical to the single launch, and the rows
@@ -682,7 +702,7 @@ def test_gemm_split_last_round(n_out, n_in, n_tok, monkeypatch):
     Wd, Xd = dev(W), dev(Xq)
     got = {}
     for split in ("1", "0"):
-        monkeypatch.setenv("BONSAI_GEMM_F16_SPLIT", split)
+        knobs.set("BONSAI_GEMM_F16_SPLIT", split)
         Y = torch.full((n_out, n_tok), float("nan"), dtype=torch.float32, device="cuda")
         B.gemm(Wd, Xd, Y, n_out, n_in, n_tok)
         got[split] = host(Y)

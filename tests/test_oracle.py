@@ -215,6 +215,73 @@ def test_rmsnorm_closed_form_and_planted_mistakes():
     assert tol(x64 / np.sqrt((x64 ** 2).sum() + eps) * w) > 1e-3
 
 
+# ------------------------------- ternary quantiser / dequantiser / dot (F9)
+def test_quantize_pq2_0_fixture(golden):
+    """Bytes of quantize_row_pq2_0 (src/pq2_0.h:74-90) on weight-like and
+    edge-case blocks: +-0.5 products (lroundf ties), zero blocks, an fp16-tie
+    scale, subnormal and overflowing scales."""
+    np.testing.assert_array_equal(O.quantize_pq2_0(golden["f9_x"]), golden["f9_w"])
+
+
+def test_quantize_pq2_0_closed_form():
+    """Independent of the restatement: d = fp16(amax) rounded half away,
+    code = clamp(round_half_away(x / amax) + 1, 0, 3) with the reciprocal
+    taken once in fp32; planted mistakes (RNE rounding, no +1 bias, d =
+    amax / 2) must fail the same comparison."""
+    x = np.concatenate([O.gen_normal(17, 4096, 0.02),
+                        np.repeat(np.float32([2.0, 1.0, -1.0, 0.5]), 32)])
+    w = O.quantize_pq2_0(x)
+    d, codes = O.pq2_fields(w)
+    xb = x.reshape(-1, 128)
+    amax = np.max(np.abs(xb), axis=1)
+    assert np.array_equal(d, [O.f32_to_f16(a) for a in amax])
+    inv = np.where(amax > 0, np.float32(1.0) / amax, np.float32(0)).astype(np.float32)
+    prod = (xb * inv[:, None]).astype(np.float32)
+    away = np.trunc(prod + np.copysign(0.5, prod)).astype(np.int64)   # exact for |prod| <= 1
+    ref = np.clip(away + 1, 0, 3)
+    assert np.array_equal(codes, ref)
+    assert np.any(prod == 0.5) and np.any(prod == -0.5)               # the tie cases are present
+    assert not np.array_equal(codes, np.clip(np.rint(prod).astype(np.int64) + 1, 0, 3))
+    assert not np.array_equal(codes, np.clip(away, 0, 3))
+    half = [O.f32_to_f16(a / 2) for a in amax]
+    assert not np.array_equal(d, half)
+
+
+def test_dequantize_pq2_0_fixture_and_closed_form(golden):
+    """dequantize_row_pq2_0 (src/pq2_0.h:62-71) bit patterns, incl. code 3
+    (+2d) rows, and the value rule (code - 1) * d from the decoded fields."""
+    wd = golden["f9_wd"]
+    y = O.dequantize_pq2_0(wd, wd.size // 34 * 128)
+    np.testing.assert_array_equal(bits(y), bits(golden["f9_deq"]))
+    d, codes = O.pq2_fields(wd)
+    assert np.any(codes == 3)
+    dv = np.array([O.f16_to_f32(h) for h in d], np.float32)
+    ref = (codes.astype(np.float32) - 1) * dv[:, None]
+    np.testing.assert_array_equal(bits(y), bits(ref.ravel()))
+    assert not np.array_equal(bits(y), bits((codes.astype(np.float32) * dv[:, None]).ravel()))
+
+
+def test_pq2_0_dot_f32_fixture_and_closed_form(golden):
+    """pq2_0_dot_f32 (src/pq2_0.h:134-142) bit patterns, and within fp32
+    rounding of the double-precision dot of the dequantised block; a
+    dropped "- 1" or a missing scale must fail the same check."""
+    wd, a = golden["f9_wd"], golden["f9_a"]
+    got = O.pq2_0_dot_f32(wd, a)
+    np.testing.assert_array_equal(bits(got), bits(golden["f9_dot"]))
+    d, codes = O.pq2_fields(wd)
+    dv = np.array([O.f16_to_f32(h) for h in d], np.float64)
+    a2 = a.reshape(-1, 128).astype(np.float64)
+    exact = ((codes.astype(np.float64) - 1) * a2).sum(axis=1) * dv
+    fin = np.isfinite(exact)
+    scale = np.abs(codes - 1.0) @ np.ones(128) * np.max(np.abs(a2), axis=1) * np.abs(dv) + 1e-30
+    err = np.abs(got[fin] - exact[fin]) / scale[fin]
+    assert np.max(err) < 1e-6
+    no_bias = (codes.astype(np.float64) * a2).sum(axis=1) * dv
+    assert np.max(np.abs(no_bias[fin] - exact[fin]) / scale[fin]) > 1e-3
+    no_scale = ((codes.astype(np.float64) - 1) * a2).sum(axis=1)
+    assert np.max(np.abs(no_scale[fin] - exact[fin]) / scale[fin]) > 1e-3
+
+
 # ------------------------------------------------- planted-mistake checks
 def test_checks_detect_planted_mistakes(golden):
     """The fixture comparisons must fail for plausible oracle mistakes."""
