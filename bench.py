@@ -301,44 +301,175 @@ def bench_token_sweep(steps, warmup, gen, mode="separate"):
     return ms, wbytes
 
 
-def cpu_baseline(sample_s: float):
-    """The reference host GEMV (oracle/_ref = reference sources compiled here;
-    the restatement oracle/liboracle.so if _ref is absent), 1 thread, on
-    17408x5120 matrices of the same distribution, for about sample_s seconds."""
-    sys.path.insert(0, ROOT)
-    import numpy as np
-    from oracle import oracle as O
-    R = O.ref()
-    n_out, n_in = N_FF, N_EMBD
-    W = O.gen_weights(77, n_out, n_in)
-    xq = O.quantize_q8_1(O.fwht(O.gen_normal(78, n_in)), True)
-    y = np.empty(n_out, np.float32)
-    if R is not None:
-        kind = "reference"
-        fn = lambda: R.ref_gemv(O._p(W, O._u8p), O._p(xq, O._u8p), O._p(y, O._f32p), n_out, n_in)  # noqa: E731
-    else:
-        kind = "port"
-        fn = lambda: O.lib().orc_gemv(O._p(W, O._u8p), O._p(xq, O._u8p), O._p(y, O._f32p), n_out, n_in, 1)  # noqa: E731
+def host_cpu():
+    """Model and core count of this host, and the threads the baseline uses
+    (the job's OMP_NUM_THREADS share where set, else every core)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    nproc = os.cpu_count() or 1
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        pass
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or nproc
+    return model, nproc, max(1, min(threads, nproc))
+
+
+def _timed(fn, seconds):
     t0 = time.perf_counter()
     n = 0
     while True:
         fn()
         n += 1
-        if time.perf_counter() - t0 >= sample_s:
+        if time.perf_counter() - t0 >= seconds:
             break
-    dt = (time.perf_counter() - t0) / n
-    return {"value": round(gemv_bytes(n_out, n_in) / dt / 1e9, 4), "unit": "GB/s", "cores": 1,
-            "kind": kind, "ms_per_gemv": round(dt * 1e3, 3),
-            "sample": f"{n} single-thread host GEMVs of 17408x5120 (pq2_0_row_dot_perm per row), "
-                      f"{n * dt:.1f} s"}
+    return (time.perf_counter() - t0) / n, n
+
+
+def cpu_baseline(sample_s: float):
+    """CPU baseline on this host's cores (a reported baseline, not a target):
+    * the reference's own host GEMV (pq2_0_row_dot_perm per row, compiled from
+      the reference sources into oracle/_ref; the restatement where _ref is
+      absent), single-threaded as the reference runs it;
+    * the oracle restatement (bit-identical output) with OpenMP over output
+      rows on all of the job's cores: `value`;
+    * the GEMM loop of tests/test_p40.cpp:449-470 on a row sample of the
+      17408x5120 prefill shape at M = 512, single-threaded and on all cores.
+    Same input distribution as the GPU runs; ~sample_s seconds in total."""
+    sys.path.insert(0, ROOT)
+    import numpy as np
+    from oracle import oracle as O
+    R = O.ref()
+    model, nproc, threads = host_cpu()
+    n_out, n_in = N_FF, N_EMBD
+    W = O.gen_weights(77, n_out, n_in)
+    xq = O.quantize_q8_1(O.fwht(O.gen_normal(78, n_in)), True)
+    y = np.empty(n_out, np.float32)
+    P = lambda a, t: O._p(a, t)  # noqa: E731
+    if R is not None:
+        kind1 = "reference"
+        one = lambda: R.ref_gemv(P(W, O._u8p), P(xq, O._u8p), P(y, O._f32p), n_out, n_in)  # noqa: E731
+    else:
+        kind1 = "port"
+        one = lambda: O.lib().orc_gemv(P(W, O._u8p), P(xq, O._u8p), P(y, O._f32p), n_out, n_in, 1)  # noqa: E731
+    many = lambda: O.lib().orc_gemv(P(W, O._u8p), P(xq, O._u8p), P(y, O._f32p), n_out, n_in, threads)  # noqa: E731
+    share = sample_s / 4
+    dt1, n1 = _timed(one, share)
+    dtn, nn = _timed(many, share)
+    gb = gemv_bytes(n_out, n_in)
+
+    # GEMM: 256 rows x 5120 x 512 tokens (the per-(row, token, chunk) loop)
+    M, rows = 512, 256
+    Xq = O.quantize_chunk_major(np.stack([O.fwht(O.gen_normal(90 + t, n_in)) for t in range(M)]))
+    Ws = W[:rows * (n_in // 128) * 34]
+    Y = np.empty((rows, M), np.float32)
+    if R is not None:
+        g1 = lambda: R.ref_gemm(P(Ws, O._u8p), P(Xq, O._u8p), P(Y, O._f32p), rows, n_in, M)  # noqa: E731
+    else:
+        g1 = lambda: O.lib().orc_gemm(P(Ws, O._u8p), P(Xq, O._u8p), P(Y, O._f32p), rows, n_in, M, 1)  # noqa: E731
+    gn = lambda: O.lib().orc_gemm(P(Ws, O._u8p), P(Xq, O._u8p), P(Y, O._f32p), rows, n_in, M, threads)  # noqa: E731
+    tg1, _ = _timed(g1, share)
+    tgn, _ = _timed(gn, share)
+    ops = 2.0 * rows * n_in * M
+    return {"value": round(gb / dtn / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "ms_per_gemv": round(dtn * 1e3, 3),
+            "sample": f"{nn} host GEMVs of 17408x5120 by the oracle restatement (bit-identical to the "
+                      f"reference's pq2_0_row_dot_perm), OpenMP over rows on {threads} threads, "
+                      f"{nn * dtn:.1f} s",
+            "host": {"cpu_model": model, "nproc": nproc, "threads_used": threads},
+            "single_thread": {"value": round(gb / dt1 / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind1,
+                              "ms_per_gemv": round(dt1 * 1e3, 3),
+                              "sample": f"{n1} single-thread host GEMVs of 17408x5120, {n1 * dt1:.1f} s"},
+            "gemm_prefill_row_sample": {
+                "shape": f"{rows} of 17408 rows x 5120, M = {M} tokens (tests/test_p40.cpp:449-470 loop)",
+                "single_thread": {"TOPS": round(ops / tg1 / 1e12, 5), "kind": kind1,
+                                  "ms": round(tg1 * 1e3, 2)},
+                "all_cores": {"TOPS": round(ops / tgn / 1e12, 5), "kind": "port", "threads": threads,
+                              "ms": round(tgn * 1e3, 2)},
+                "full_shape_ms_all_cores": round(tgn * 1e3 * n_out / rows, 1)}}
+
+
+def bench_sustained_read(gb: float = 2.0, reps: int = 5):
+    """Sustained HBM read: one launch over a gb-GB buffer with 8 workgroups of
+    256 lanes per CU (tools/bwtest.cu:37-47,133), HIP events around each
+    launch on the current stream; the best of reps."""
+    nbytes = int(gb * (1 << 30)) // 256 * 256
+    buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    blocks = 8 * cus
+    out = torch.zeros(blocks, dtype=torch.int32, device="cuda")
+    B.stream_read(buf, nbytes, out, blocks)
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        B.stream_read(buf, nbytes, out, blocks)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1)
+        best = ms if best is None else min(best, ms)
+    del buf
+    return nbytes, best
+
+
+def mfma_peak(kind: int, iters: int = 4096, per_cu: int = 4):
+    """MFMA peak probe (bonsai_p40_mfma_probe): per_cu 4-wave workgroups per
+    CU, each wave iters * 4 independent back-to-back MFMAs.  Returns (TOPS by
+    HIP events around the launch, shader clock in MHz from the waves' cycle
+    counters over the same time)."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    blocks = per_cu * cus
+    clk = torch.zeros(2 * blocks, dtype=torch.int64, device="cuda")
+    sink = torch.zeros(blocks, dtype=torch.int32, device="cuda")
+    B.mfma_probe(kind, blocks, 64, clk, sink)
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        B.mfma_probe(kind, blocks, iters, clk, sink)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1)
+        if best is None or ms < best[0]:
+            best = (ms, clk.cpu())
+    ms, c = best
+    ops_per = 32768 if kind == 0 else 16384
+    ops = float(blocks) * 4 * iters * 4 * ops_per
+    cycles = c.view(-1, 2)[:, 0].double().median().item()
+    return ops / (ms * 1e-3) / 1e12, cycles / (ms * 1e3)
+
+
+def kernel_source_hash():
+    """sha256 over the device sources that build the decode GEMV kernel: a
+    traffic figure measured on another build of them is not reported."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in ("gemv.hip", "pq2_device.h", "fwht_device.h"):
+        with open(os.path.join(ROOT, "p40-kernel_amd", "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
 
 
 def load_traffic(path):
+    """The PMC traffic record of the decode GEMV kernel, if it was measured on
+    the current kernel sources (else None and the reason)."""
     try:
         with open(path) as f:
-            return json.load(f)
+            t = json.load(f)
     except (OSError, ValueError):
-        return None
+        return None, "no PMC record"
+    if t.get("source_sha256") != kernel_source_hash():
+        return None, "PMC record measured on other kernel sources"
+    return t, None
 
 
 def main():
@@ -348,7 +479,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only (no secondary configs)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=16.0)
     ap.add_argument("--only-gemv", action="store_true", help="headline GEMV loop only (profiling)")
     ap.add_argument("--eager", action="store_true",
                     help="time Python launches one by one instead of replaying HIP graphs")
@@ -433,6 +564,21 @@ def main():
                                        "note": "plain 16-byte streaming read of 23,750,272 B per launch: "
                                                "the achievable ceiling for one launch of this size"}
     print(f"[bench] stream read ceiling: {extra['stream_read_same_bytes']}", file=sys.stderr, flush=True)
+    sb, sms = bench_sustained_read()
+    sus_gbs = sb / (sms * 1e-3) / 1e9
+    extra["stream_read_sustained"] = {"bytes": sb, "us": round(sms * 1e3, 1), "GB/s": round(sus_gbs, 1),
+                                      "frac_hbm_peak": round(sus_gbs / HBM_PEAK_GBS, 4),
+                                      "note": "one launch over 2 GiB, 8 workgroups per CU: sustained HBM read"}
+    print(f"[bench] sustained read: {extra['stream_read_sustained']}", file=sys.stderr, flush=True)
+    peaks = {}
+    for kind, name in ((0, "int8"), (1, "f16")):
+        tops, mhz = mfma_peak(kind)
+        peaks[name] = {"TOPS": round(tops, 1), "clock_MHz": round(mhz, 0)}
+    extra["mfma_peak_probe"] = {
+        **peaks, "published_dense": {"int8": INT8_PEAK_TOPS, "f16": 2500.0},
+        "note": "back-to-back independent v_mfma_i32_16x16x64_i8 / v_mfma_f32_16x16x32_f16, "
+                "16 waves per CU; clock = waves' shader cycles over the launch time"}
+    print(f"[bench] mfma peak: {extra['mfma_peak_probe']}", file=sys.stderr, flush=True)
     if not args.quick:
         for (n_out, n_in, tag) in ((N_EMBD, N_FF, "gemv_5120x17408"), (N_EMBD, N_EMBD, "gemv_5120x5120")):
             m = bench_gemv(n_out, n_in, args.steps, args.warmup, gen)
@@ -500,17 +646,22 @@ def main():
             for (n_out, n_in) in ((N_FF, N_EMBD), (N_EMBD, N_FF)):
                 m = bench_gemv(n_out, n_in, 10, 3, gen, n_tok=M)
                 tops = 2.0 * M * n_out * n_in / (m * 1e-3) / 1e12
-                extra[f"prefill_M{M}_{n_out}x{n_in}"] = {"us": round(m * 1e3, 1), "TOPS": round(tops, 1),
-                                                         "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+                extra[f"prefill_M{M}_{n_out}x{n_in}"] = {
+                    "us": round(m * 1e3, 1), "TOPS": round(tops, 1),
+                    "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                    "frac_int8_probe": round(tops / peaks["int8"]["TOPS"], 4)}
                 print(f"[bench] prefill M={M} {n_out}x{n_in}: {extra[f'prefill_M{M}_{n_out}x{n_in}']}",
                       file=sys.stderr, flush=True)
 
-    traffic = load_traffic(os.path.join(ROOT, "profiles", "gemv_17408x5120_traffic.json"))
+    traffic, why = load_traffic(os.path.join(ROOT, "profiles", "gemv_17408x5120_traffic.json"))
     roof = {"bound": "hbm", "kernel": "gemv_nb_kernel<40, 2, 4> (bonsai_p40_gemv)",
             "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "frac_of_achievable": round(gbs / read_gbs, 4),
+            "frac_of_achievable": round(gbs / sus_gbs, 4),
+            "frac_of_single_launch_read": round(gbs / read_gbs, 4),
             "traffic": traffic.get("bytes_per_launch") if traffic else None,
+            "traffic_source": (f"profiles/gemv_17408x5120_traffic.json (kernel sources {traffic['source_sha256']})"
+                               if traffic else why),
             "algorithmic_bytes": nbytes}
     cpu = None
     if not args.no_cpu:

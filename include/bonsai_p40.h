@@ -223,6 +223,16 @@ int bonsai_p40_reload_tuning(void);
 int bonsai_p40_stream_read(const void * buf, int64_t bytes, uint32_t * out, int blocks,
                            bonsai_stream stream);
 
+// Measurement helper: MFMA peak probe.  `blocks` workgroups of 4 waves, each
+// wave issuing iters * 4 independent back-to-back MFMAs of one kind (0 = int8
+// v_mfma_i32_16x16x64_i8, 32768 ops each; 1 = f16 v_mfma_f32_16x16x32_f16,
+// 16384 ops each).  clk (2 * blocks words) receives, per workgroup, the
+// shader-clock and real-time (hipDeviceAttributeWallClockRate) deltas of its
+// first wave's loop, from which the clock the MFMAs ran at follows.  sink
+// needs `blocks` words.  Errors: 1 on bad arguments.
+int bonsai_p40_mfma_probe(int kind, int blocks, int iters, uint64_t * clk, uint32_t * sink,
+                          bonsai_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

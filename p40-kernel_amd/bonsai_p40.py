@@ -50,6 +50,7 @@ SIGNATURES = {
     "bonsai_p40_chunk_dots": [_V, _V, _V, _I64, _I64, _V],
     "bonsai_p40_stream_read": [_V, _I64, _V, C.c_int, _V],
     "bonsai_p40_reload_tuning": [],
+    "bonsai_p40_mfma_probe": [C.c_int, C.c_int, C.c_int, _V, _V, _V],
 }
 
 _lib = None
@@ -221,6 +222,10 @@ def chunk_dots(W, xq, out, n_out: int, n_in: int, stream=None) -> None:
 def reload_tuning() -> None:
     """Re-read the BONSAI_* tuning variables after changing os.environ."""
     _check("bonsai_p40_reload_tuning", lib().bonsai_p40_reload_tuning())
+
+
+def mfma_probe(kind: int, blocks: int, iters: int, clk, sink, stream=None) -> None:
+    _check("bonsai_p40_mfma_probe", call("bonsai_p40_mfma_probe", kind, blocks, iters, clk, sink, stream=stream))
 
 
 def stream_read(buf, nbytes: int, out, blocks: int, stream=None) -> None:

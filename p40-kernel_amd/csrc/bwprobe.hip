@@ -1,8 +1,13 @@
-// bwprobe.hip -- HBM streaming-read ceiling probe (the analog of the
-// reference's tools/bwtest.cu read_kernel, tools/bwtest.cu:37-47): every
-// lane reads 16-byte vectors grid-stride and folds them with XOR, one word
-// per workgroup is written so the loads cannot be elided.  Used by bench.py to
-// report "% of achievable" next to "% of peak".
+// bwprobe.hip -- measurement probes used by bench.py to report "% of
+// achievable" next to "% of peak":
+//  * HBM streaming-read ceiling (the analog of the reference's tools/bwtest.cu
+//    read_kernel, tools/bwtest.cu:37-47): every lane reads 16-byte vectors
+//    grid-stride and folds them with XOR, one word per workgroup is written so
+//    the loads cannot be elided;
+//  * MFMA peak: back-to-back independent int8 (v_mfma_i32_16x16x64_i8) or f16
+//    (v_mfma_f32_16x16x32_f16) matrix instructions, with each wave's shader
+//    clock and real-time counters read around its loop so the host can derive
+//    the clock the MFMAs ran at.
 #include "pq2_device.h"
 #include "../../include/bonsai_p40.h"
 
@@ -27,7 +32,84 @@ stream_read_kernel(const v4u * __restrict__ src, size_t n16, uint32_t * __restri
     if (v == 0x9e3779b9u) out[blockIdx.x] = v;   // practically never true; keeps the loads live
 }
 
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int PROBE_ACC = 4;        // independent accumulators per wave (more get shuffled)
+
+// KIND 0: int8 16x16x64 (32768 ops per instruction), KIND 1: f16 16x16x32
+// (16384 ops).  Each wave issues iters * PROBE_ACC MFMAs in chains of
+// PROBE_ACC independent accumulators.  Wave 0 of each workgroup records its
+// shader-clock and real-time deltas in clk[2 * blockIdx.x + {0, 1}].
+template <int KIND>
+__global__ void __launch_bounds__(256)
+mfma_probe_kernel(int iters, uint64_t * __restrict__ clk, uint32_t * __restrict__ sink) {
+    const int lane = threadIdx.x & 63;
+    v4i ai = {lane, lane * 3, lane ^ 5, 7};
+    v4i bi = {lane + 1, lane * 5, lane ^ 9, 3};
+    v8h ah, bh;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        ah[k] = (_Float16)(0.001f * (float)(lane + k));
+        bh[k] = (_Float16)(0.002f * (float)(lane - k));
+    }
+    v4i acci[PROBE_ACC];
+    v4f accf[PROBE_ACC];
+    // distinct lane-dependent starting values: accumulators that start equal
+    // get coalesced by the compiler into shuffled register copies in the loop
+#pragma unroll
+    for (int k = 0; k < PROBE_ACC; ++k) {
+        acci[k] = (v4i){lane + k, lane * (k + 2), lane ^ (k + 1), 3 * k - lane};
+        accf[k] = (v4f){(float)(lane + k), (float)(lane * (k + 2)), (float)(lane ^ (k + 1)),
+                        (float)(3 * k - lane)};
+    }
+    const uint64_t c0 = __builtin_readcyclecounter();
+    const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
+    for (int i = 0; i < iters; ++i) {
+#pragma unroll
+        for (int k = 0; k < PROBE_ACC; ++k) {
+            if constexpr (KIND == 0)
+                acci[k] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ai, bi, acci[k], 0, 0, 0);
+            else
+                accf[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, accf[k], 0, 0, 0);
+        }
+    }
+    // the deltas are read after the last MFMA's result is consumed
+    uint32_t fold = 0;
+#pragma unroll
+    for (int k = 0; k < PROBE_ACC; ++k) {
+        if constexpr (KIND == 0) fold ^= (uint32_t)(acci[k][0] ^ acci[k][1] ^ acci[k][2] ^ acci[k][3]);
+        else fold ^= __float_as_uint(accf[k][0] + accf[k][1] + accf[k][2] + accf[k][3]);
+    }
+    fold = __builtin_amdgcn_readfirstlane(fold);
+    const uint64_t c1 = __builtin_readcyclecounter();
+    const uint64_t r1 = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0) {
+        clk[2 * blockIdx.x] = c1 - c0;
+        clk[2 * blockIdx.x + 1] = r1 - r0;
+    }
+    if (fold == 0x9e3779b9u) sink[blockIdx.x] = fold;   // keeps the MFMAs live
+}
+
 }  // namespace
+
+// MFMA peak probe: `blocks` workgroups of 4 waves, each wave issuing iters *
+// 4 MFMAs of the chosen kind (0: int8 16x16x64, 1: f16 16x16x32).  clk needs
+// 2 * blocks words (shader-clock and real-time deltas of each workgroup's
+// wave 0), sink `blocks` words (written only in a practically impossible
+// case).  Errors: 1 on bad arguments.
+extern "C" int bonsai_p40_mfma_probe(int kind, int blocks, int iters, uint64_t * clk, uint32_t * sink,
+                                     bonsai_stream stream) {
+    if (blocks <= 0 || iters <= 0 || clk == nullptr || sink == nullptr || (kind != 0 && kind != 1)) return 1;
+    if (kind == 0)
+        hipLaunchKernelGGL(mfma_probe_kernel<0>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, iters,
+                           clk, sink);
+    else
+        hipLaunchKernelGGL(mfma_probe_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, iters,
+                           clk, sink);
+    return (int)hipGetLastError();
+}
 
 extern "C" int bonsai_p40_stream_read(const void * buf, int64_t bytes, uint32_t * out, int blocks,
                                       bonsai_stream stream) {

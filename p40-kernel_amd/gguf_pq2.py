@@ -282,12 +282,13 @@ def check_geometry(h: GGUFHeader):
     number of layers match; names matching nextn/mtp/draft/eagle fail the
     file (the engine has no MTP layer)."""
     fails, rep = [], []
+    rep.append("metadata keys:")
     for k, want in EXPECT_KV.items():
         got = h.kv.get(k) if h.kv_types.get(k) in _CHECKED_KV_TYPES else None
         ok = got == want
-        rep.append(f"  {'OK ' if ok else 'BAD'} {k} = {got}")
+        rep.append(f"  [{'pass' if ok else 'FAIL'}] key {k}: found {got!r}, engine needs {want!r}")
         if not ok:
-            fails.append(f"{k}: got {got}, want {want}")
+            fails.append(f"metadata key {k} is {got!r}; the engine is built for {want!r}")
 
     groups: dict = {}
     mtp = []
@@ -297,9 +298,10 @@ def check_geometry(h: GGUFHeader):
         key = (t.generic_name, t.dims, t.type)
         groups[key] = groups.get(key, 0) + 1
     if h.truncated:
-        rep.append(f"  (partial header, tensor list truncated: {h.truncated})")
+        rep.append(f"  note: only part of the header was readable ({h.truncated}); "
+                   "tensors past that point were not checked")
 
-    rep.append("tensor type/geometry checks:")
+    rep.append("tensor groups (name pattern, shape, type, layers):")
     for (g, dims, tt), cnt in sorted(groups.items()):
         exp = EXPECT_TENSORS.get(g)
         if exp is None:
@@ -309,19 +311,22 @@ def check_geometry(h: GGUFHeader):
         ok = (len(dims) >= 1 and dims[0] == n_in
               and (n_out is None or (len(dims) >= 2 and dims[1] == n_out))
               and tt == etype and (want_count is None or cnt == want_count))
-        rep.append(f"  {'OK ' if ok else 'BAD'} {g:32s} dims={list(dims)} type={tt} x{cnt}")
+        rep.append(f"  [{'pass' if ok else 'FAIL'}] {g}: shape {list(dims)}, type {tt}, {cnt} of them")
         if not ok:
-            fails.append(f"{g}: dims={list(dims)} type={tt} x{cnt}, "
-                         f"want ({n_in},{n_out}) type={etype} x{want_count}")
+            need_shape = f"[{n_in}, {n_out}]" if n_out is not None else f"[{n_in}, *]"
+            need_count = f", {want_count} of them" if want_count is not None else ""
+            fails.append(f"tensor group {g} is shape {list(dims)}, type {tt}, {cnt} of them; "
+                         f"the engine needs shape {need_shape}, type {etype}{need_count}")
 
     if mtp:
-        rep.append(f"MTP/nextn block detected: {len(mtp)} tensors")
-        rep.extend(f"  e.g. {n}" for n in mtp[:6])
-        fails.append("this file carries an MTP (nextn) block; the engine has no MTP layer, "
-                     "no small-batch verify path and no second cache stream. The trunk "
-                     "weights are still valid, but a context that uses MTP cannot be built.")
+        rep.append(f"multi-token-prediction tensors present: {len(mtp)}")
+        rep.extend(f"  for instance {n}" for n in mtp[:6])
+        fails.append(f"{len(mtp)} multi-token-prediction (nextn) tensors found: this engine runs "
+                     "the trunk only, with no draft layer, no batched verification and no second "
+                     "KV stream, so a model that needs them cannot run here (its trunk tensors "
+                     "are otherwise usable)")
     else:
-        rep.append("MTP/nextn block: none (trunk-only file, matches the engine)")
+        rep.append("multi-token-prediction tensors: none, the file is trunk-only as the engine expects")
     return fails, rep
 
 
@@ -526,18 +531,18 @@ def main(argv=None) -> int:
         try:
             h = read_header(buf, partial=True)
         except GGUFError as e:
-            print(f"FAILED (1):\n  - {e}")
+            print(f"not usable by this engine: 1 problem\n  * {e}")
             return 1
-        print(f"GGUF v{h.version}  tensors={h.n_tensors}  kv={len(h.kv)}")
+        print(f"{path}: GGUF version {h.version}, {h.n_tensors} tensors, {len(h.kv)} metadata keys")
         fails, rep = check_geometry(h)
         print("\n".join(rep))
         print()
         if fails:
-            print(f"FAILED ({len(fails)}):")
+            print(f"not usable by this engine: {len(fails)} problem{'s' if len(fails) > 1 else ''}")
             for m in fails:
-                print("  -", m)
+                print("  *", m)
             return 1
-        print("All GGUF geometry checks passed.")
+        print("usable: every key and tensor group matches the engine's geometry")
         return 0
     finally:
         _close(buf)

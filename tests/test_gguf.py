@@ -109,8 +109,8 @@ def test_truncated_header():
         G.read_header(full[:200], partial=True)
     # a cut list fails the counted groups (fewer layers than the engine needs)
     fails = G.check_geometry(hp)[0]
-    assert any(f.startswith("blk.X.attn_norm.weight") for f in fails)
-    assert not any(f.startswith("general.") or f.startswith("qwen35.") for f in fails)
+    assert any("group blk.X.attn_norm.weight " in f for f in fails)
+    assert not any(f.startswith("metadata key") for f in fails)
     assert G.check_loadable(hp, len(cut)) == [f"tensor list incomplete: {hp.truncated}"]
 
 
@@ -119,8 +119,9 @@ def test_full_27b_geometry_passes():
     h = G.read_header(S.bonsai27b_header())
     fails, rep = G.check_geometry(h)
     assert fails == []
-    assert sum(1 for r in rep if r.startswith("  OK ")) == len(G.EXPECT_KV) + len(G.EXPECT_TENSORS)
-    assert rep[-1].startswith("MTP/nextn block: none")
+    assert sum(1 for r in rep if r.startswith("  [pass]")) == len(G.EXPECT_KV) + len(G.EXPECT_TENSORS)
+    assert not any(r.startswith("  [FAIL]") for r in rep)
+    assert rep[-1].startswith("multi-token-prediction tensors: none")
 
 
 def _mutate_tensors(fn):
@@ -161,7 +162,7 @@ PLANTED = {
     "one up missing": (dict(tensors=_mutate_tensors(
         lambda t: None if t[0] == "blk.3.ffn_up.weight" else t)), []),
     "mtp block": (dict(tensors=S.bonsai27b_tensors() + [("blk.64.nextn.eh_proj.weight", (10240, 5120),
-                                                          S.PQ2, None)]), ["MTP"]),
+                                                          S.PQ2, None)]), ["nextn"]),
     # tensors the engine does not check are ignored
     "extra tensor": (dict(tensors=S.bonsai27b_tensors() + [("rope_freqs.weight", (32,), S.F32, None)]),
                      []),
@@ -181,13 +182,14 @@ def test_cli(tmp_path, capsys):
     p = tmp_path / "head.bin"
     p.write_bytes(S.bonsai27b_header())
     assert G.main([str(p)]) == 0
-    assert "All GGUF geometry checks passed." in capsys.readouterr().out
+    assert "usable: every key and tensor group matches" in capsys.readouterr().out
     assert G.main(["--header", str(p)]) == 0
     capsys.readouterr()
     p.write_bytes(S.bonsai27b_header(kv_override={"qwen35.block_count": (S.T_U32, 32)}))
     assert G.main([str(p)]) == 1
     out = capsys.readouterr().out
-    assert "FAILED (1):" in out and "qwen35.block_count: got 32, want 64" in out
+    assert "not usable by this engine: 1 problem" in out
+    assert "metadata key qwen35.block_count is 32; the engine is built for 64" in out
     p.write_bytes(b"NOPE" + bytes(20))
     assert G.main([str(p)]) == 1
     assert G.main([]) == 2
