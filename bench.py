@@ -268,9 +268,18 @@ def bench_token_sweep(steps, warmup, gen, mode="separate"):
     yk, yv, yg, yu = (torch.empty(n, device="cuda") for n in (KV_DIM, KV_DIM, N_FF, N_FF))
 
     nw = torch.randn(N_EMBD, generator=gen, device="cuda") * 0.1 + 1
+    ws = torch.zeros(B.ffn_workspace_bytes(N_FF), dtype=torch.uint8, device="cuda")
 
     def token(i):
         for L in layers:
+            if mode == "layer_ffn":
+                Wq, Wk, Wv, Wo, Wg, Wu, Wd = L
+                B.rmsnorm_fwht_gemv_group([Wq, Wk, Wv], xs[N_EMBD], nw, None, [ys[Q_DIM], yk, yv],
+                                          [Q_DIM, KV_DIM, KV_DIM], N_EMBD, 1e-6)
+                B.fwht_gemv(Wo, xs[Q_DIM], None, ys[N_EMBD], N_EMBD, Q_DIM)
+                B.ffn_gate_up_swiglu(Wg, Wu, xs[N_EMBD], nw, None, None, qs[N_FF], N_FF, N_EMBD, 1e-6, ws)
+                B.gemv(Wd, qs[N_FF], ys[N_EMBD], N_EMBD, N_FF)
+                continue
             if mode == "layer":
                 Wq, Wk, Wv, Wo, Wg, Wu, Wd = L
                 B.rmsnorm_fwht_gemv_group([Wq, Wk, Wv], xs[N_EMBD], nw, None, [ys[Q_DIM], yk, yv],
@@ -491,7 +500,7 @@ def main():
                     help="small-batch GEMM 17408x5120 with B tokens only (profiling)")
     ap.add_argument("--only-fused", action="store_true",
                     help="fused FWHT+Q8_1+GEMV 17408x5120 from fp32 only (profiling)")
-    ap.add_argument("--only-sweep", default="", metavar="MODE", choices=["", "separate", "fused", "grouped", "layer"],
+    ap.add_argument("--only-sweep", default="", metavar="MODE", choices=["", "separate", "fused", "grouped", "layer", "layer_ffn"],
                     help="config-2 token sweep in one mode only (profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -629,7 +638,9 @@ def main():
                            ("grouped", "q/k/v and gate/up as grouped fused launches, o fused, "
                                        "down with its pre-pass: 4 GEMV launches + 1 pre-pass per layer"),
                            ("layer", "as grouped, with both layer RMSNorms inside the grouped launches "
-                                     "and SwiGLU+FWHT+Q8_1 of the gate/up outputs feeding down")):
+                                     "and SwiGLU+FWHT+Q8_1 of the gate/up outputs feeding down"),
+                           ("layer_ffn", "as layer, with the SwiGLU+FWHT+Q8_1 glue inside the gate/up launch "
+                                         "(bonsai_p40_ffn_gate_up_swiglu): 4 launches per layer")):
             m, wb = bench_token_sweep(5, 2, gen, mode=mode)
             extra[f"token_sweep_config2_{mode}"] = {"ms_per_token": round(m, 3), "tok/s": round(1e3 / m, 2),
                                                     "weight_GB/s": round(wb / (m * 1e-3) / 1e9, 1),

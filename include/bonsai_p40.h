@@ -190,6 +190,32 @@ int bonsai_p40_rmsnorm_fwht_gemv_group(const void * const * W, float * const * y
                                        int n_mat, const float * x, const float * norm_w, const float * signs,
                                        int64_t n_in, float eps, bonsai_stream stream);
 
+// FFN gate/up with its SwiGLU glue in one launch (src/ops.h:27-31 after the
+// gate and up GEMVs):  hq = Q8_1(FWHT(h_signs .* silu(Wg . a) * (Wu . a)))
+// with a = Q8_1(FWHT(x_signs .* RMSNorm(x, norm_w, eps))) (norm_w NULL: no
+// RMSNorm).  In place of bonsai_p40_rmsnorm_fwht_gemv_group on {Wg, Wu}
+// followed by bonsai_p40_swiglu_fwht_quant (the reference runs rmsnorm, fwht,
+// quant_activations, two gemv and the glue as separate kernels); hq is the
+// same bytes, ready for the down projection's bonsai_p40_gemv.  Wg and Wu are
+// n_ff x n_embd PQ2_0; x, norm_w, x_signs have n_embd floats, h_signs n_ff
+// (signs may be NULL); hq has n_ff/32 Q8_1 blocks.
+// workspace: BONSAI_P40_FFN_WORKSPACE_BYTES(n_ff) device bytes, 16-byte
+// aligned, ZERO-FILLED before its first use.  Its first
+// BONSAI_P40_FFN_SYNC_BYTES hold the launch's completion counters, which a
+// completed call leaves ready for the next one (do not modify them between
+// calls); the gate and up rows (fp32) follow.  Calls that may run at the
+// same time need their own workspaces.  status (device, may be NULL): the
+// kernel adds 1 for each internal wait that gave up (it then leaves hq partly
+// unwritten and the workspace must be zero-filled again).  Errors: 1 if a
+// pointer is NULL or misaligned, n_ff or n_embd <= 0 or not a multiple of
+// 1024.
+#define BONSAI_P40_FFN_SYNC_BYTES 256
+#define BONSAI_P40_FFN_WORKSPACE_BYTES(n_ff) (BONSAI_P40_FFN_SYNC_BYTES + 8 * (int64_t)(n_ff))
+int bonsai_p40_ffn_gate_up_swiglu(const void * Wg, const void * Wu, const float * x, const float * norm_w,
+                                  const float * x_signs, const float * h_signs, void * hq, int64_t n_ff,
+                                  int64_t n_embd, float eps, void * workspace, uint32_t * status,
+                                  bonsai_stream stream);
+
 // Reference ternary weight quantiser: n fp32 weights (n % 128 == 0, rows of a
 // matrix back to back) -> n/128 block_pq2_0 with d = amax rounded to fp16
 // half away from zero and code = clamp(lroundf(x / amax) + 1, 0, 3); bytes

@@ -45,6 +45,7 @@ SIGNATURES = {
     "bonsai_p40_gemv_group": [_V, _V, _V, C.c_int, _V, _I64, _V],
     "bonsai_p40_fwht_gemv_group": [_V, _V, _V, C.c_int, _F32P, _F32P, _I64, _V],
     "bonsai_p40_rmsnorm_fwht_gemv_group": [_V, _V, _V, C.c_int, _F32P, _F32P, _F32P, _I64, C.c_float, _V],
+    "bonsai_p40_ffn_gate_up_swiglu": [_V, _V, _F32P, _F32P, _F32P, _F32P, _V, _I64, _I64, C.c_float, _V, _V, _V],
     "bonsai_p40_quantize_pq2_0": [_F32P, _V, _I64, _V],
     "bonsai_p40_dequantize_pq2_0": [_V, _F32P, _I64, _V],
     "bonsai_p40_chunk_dots": [_V, _V, _V, _I64, _I64, _V],
@@ -204,6 +205,24 @@ def rmsnorm_fwht_gemv_group(Ws, x, norm_w, signs, ys, n_outs, n_in: int, eps: fl
                                                   C.c_float(eps), _stream(stream))
     del keep
     _check("bonsai_p40_rmsnorm_fwht_gemv_group", rc)
+
+
+FFN_SYNC_BYTES = 256
+
+
+def ffn_workspace_bytes(n_ff: int) -> int:
+    """BONSAI_P40_FFN_WORKSPACE_BYTES(n_ff) of include/bonsai_p40.h."""
+    return FFN_SYNC_BYTES + 8 * n_ff
+
+
+def ffn_gate_up_swiglu(Wg, Wu, x, norm_w, x_signs, h_signs, hq, n_ff: int, n_embd: int, eps: float,
+                       workspace, status=None, stream=None) -> None:
+    """hq = Q8_1(FWHT(h_signs .* swiglu(Wg.a, Wu.a))), a = Q8_1(FWHT(x_signs .*
+    RMSNorm(x))) (norm_w None: no RMSNorm), one launch; workspace zero-filled
+    before its first use (ffn_workspace_bytes(n_ff) bytes)."""
+    _check("bonsai_p40_ffn_gate_up_swiglu",
+           call("bonsai_p40_ffn_gate_up_swiglu", Wg, Wu, x, norm_w, x_signs, h_signs, hq, n_ff, n_embd,
+                C.c_float(eps), workspace, status, stream=stream))
 
 
 def quantize_pq2_0(x, w, n: int, stream=None) -> None:

@@ -161,6 +161,16 @@ __device__ __forceinline__ void fwht1024_regs(float (&v)[16], int l) {
     for (int r = 0; r < 16; ++r) v[r] = v[r] * scale;
 }
 
+// SwiGLU of one element, silu(g) * u with silu(g) = g / (1 + exp(-g))
+// (src/ops.h:27-31): one rounded division and one rounded product, no
+// contraction.  The FFN glue kernels all use this, so their values agree bit
+// for bit.
+__device__ __forceinline__ float swiglu1(float g, float u) {
+#pragma clang fp contract(off)
+    const float s = g / (1.0f + expf(-g));
+    return s * u;
+}
+
 // Quantise the 32-element chunk held by the lane pair (l, l^1), 16 elements
 // per lane, and store it as one block_q8_1 at `blk` (4-byte aligned, global or
 // LDS).  d = amax/127 (IEEE division), id = 1/d or 0, q = round-half-away(x*id)

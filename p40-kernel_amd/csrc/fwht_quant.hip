@@ -38,7 +38,6 @@ enum : int {
     M_VEC = 64,       // 16-byte aligned fp32 pointers: dwordx4 loads/stores
 };
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
 // Grid (n/1024, n_tok), 64 threads.  `x` is [n_tok][n].  Block b reads its
 // signs at signs + b * sign_stride: 1024 for a length-n vector (the host
@@ -200,7 +199,7 @@ rms_rot_quant_block_kernel(const float * __restrict__ x, const float * __restric
 // SwiGLU (an expf and an IEEE division per element, the bulk of the work) is
 // spread over all 256 threads, 4 elements each, into LDS; wave 0 then loads
 // the block in the FWHT lane layout, applies the signs, rotates and
-// quantises.  Element values are those of the one-wave kernel (same silu()).
+// quantises.  Element values are swiglu1() of fwht_device.h.
 template <bool VEC, bool SIGNS>
 __global__ void __launch_bounds__(256)
 swiglu_rot_quant_kernel(const float * __restrict__ gate, const float * __restrict__ up,
@@ -219,7 +218,7 @@ swiglu_rot_quant_kernel(const float * __restrict__ gate, const float * __restric
         for (int k = 0; k < 4; ++k) { g[k] = gate[base + 4 * tid + k]; u[k] = up[base + 4 * tid + k]; }
     }
     float4 r;
-    r.x = silu(g[0]) * u[0]; r.y = silu(g[1]) * u[1]; r.z = silu(g[2]) * u[2]; r.w = silu(g[3]) * u[3];
+    r.x = swiglu1(g[0], u[0]); r.y = swiglu1(g[1], u[1]); r.z = swiglu1(g[2], u[2]); r.w = swiglu1(g[3], u[3]);
     reinterpret_cast<float4 *>(h)[tid] = r;
     __syncthreads();
     if (tid >= 64) return;

@@ -261,6 +261,19 @@ __device__ __forceinline__ float wave_sum2_to_lanes31_63(float acc0, float acc1)
 // counted on their own (its last unit may hold fewer than G rows), so no
 // unit straddles two matrices.
 constexpr int MAX_GROUP = 4;
+// FFN epilogue of the gate/up group (EPI kernels only): once every workgroup
+// has stored its gate (y[0]) and up (y[1]) rows, hq = Q8_1(FWHT(h_signs .*
+// swiglu(gate, up))) per 1024-block.  sync[0] counts workgroups that stored
+// their rows (zero before a launch and again after it), sync[1] is a
+// generation number advanced once per launch.  status (may be null) counts
+// waits that gave up.
+struct FfnEpilogue {
+    uint32_t * sync;
+    const float * h_signs;
+    uint8_t * hq;
+    uint32_t * status;
+    int nblk;                   // 1024-blocks of the gate/up rows
+};
 struct MatGroup {
     const uint8_t * W[MAX_GROUP];
     float * y[MAX_GROUP];
@@ -268,6 +281,7 @@ struct MatGroup {
     int u0[MAX_GROUP + 1];
     const float * norm_w;       // RMSNorm weights of the fused rotation (RMS kernels only)
     float eps;
+    FfnEpilogue epi;
 };
 
 MatGroup single_group(const void * W, float * y, int64_t n_out) {
@@ -346,6 +360,93 @@ __device__ __forceinline__ double * rms_partials() {
     return buf;
 }
 
+// Polls of the FFN epilogue's wait before it gives up (each poll is one
+// device-coherent load plus a short sleep: some tens of milliseconds in all).
+constexpr uint32_t EPI_SPIN_LIMIT = 1u << 16;
+
+// FFN epilogue of the gate/up group kernel (src/ops.h:27-31 after the two
+// GEMVs).  Every workgroup read the generation word sync[1] when it started
+// (gen0: nothing advances it before every workgroup has taken its ticket),
+// stored its gate and up rows with device-coherent stores, waits for their
+// acknowledgement and takes one ticket from sync[0].  The workgroup holding the
+// last ticket zeroes sync[0] and then advances sync[1]: every row of both
+// matrices is in memory from then on.  The workgroups holding the last
+// nfin = min(#workgroups, nblk) tickets are the finalisers: each waits
+// (bounded) for sync[1] to move past the value it read (the last one does
+// not wait), then finishes the 1024-blocks f, f + nfin, ...: SwiGLU of the
+// block over all its threads into LDS (device-coherent loads), then one wave
+// applies the signs, rotates (fwht1024_regs) and quantises
+// (quant_pair_store) -- the device code of bonsai_p40_swiglu_fwht_quant, so
+// hq is the same bytes.  A finaliser whose wait gives up adds 1 to *status
+// and leaves its blocks unwritten.  Non-finalising workgroups leave right
+// after their ticket, which frees their CUs for any workgroup not yet
+// started, so the wait always ends.
+template <int WAVES>
+__device__ __forceinline__ void ffn_epilogue(const MatGroup & mg, float * h_lds, uint32_t gen0) {
+    const FfnEpilogue & e = mg.epi;
+    __shared__ uint32_t epi_ticket, epi_gave_up;
+    wait_vmcnt<0>();                                   // this wave's rows are acknowledged
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    const uint32_t nwg = gridDim.x;
+    const uint32_t nfin = nwg < (uint32_t)e.nblk ? nwg : (uint32_t)e.nblk;
+    if (threadIdx.x == 0) {
+        const uint32_t t = __hip_atomic_fetch_add(&e.sync[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t give = 0;
+        if (t == nwg - 1) {
+            // every workgroup's rows are acknowledged: reset the ticket counter
+            // for the next launch (nothing reads it again in this one) and open
+            // the finalisers' wait
+            __hip_atomic_store(&e.sync[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&e.sync[1], gen0 + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else if (t >= nwg - nfin) {
+            uint32_t polls = 0;
+            while (__hip_atomic_load(&e.sync[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen0) {
+                if (++polls > EPI_SPIN_LIMIT) {
+                    give = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        epi_ticket = t;
+        epi_gave_up = give;
+    }
+    __syncthreads();
+    const uint32_t t = epi_ticket;
+    if (t < nwg - nfin) return;
+    if (epi_gave_up) {
+        if (threadIdx.x == 0 && e.status != nullptr)
+            __hip_atomic_fetch_add(e.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    for (int b = (int)(t - (nwg - nfin)); b < e.nblk; b += (int)nfin) {
+        const float * g = mg.y[0] + (size_t)HBLK * b;
+        const float * u = mg.y[1] + (size_t)HBLK * b;
+        for (int i = threadIdx.x; i < HBLK; i += 64 * WAVES) {
+            const float gv = __hip_atomic_load(g + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float uv = __hip_atomic_load(u + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            h_lds[i] = swiglu1(gv, uv);
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            const int l = threadIdx.x, row = fwht_row(l);
+            float v[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) v[r] = h_lds[16 * row + r];
+            if (e.h_signs != nullptr) {
+                const float * sg = e.h_signs + (size_t)HBLK * b + 16 * row;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) v[r] *= sg[r];
+            }
+            fwht1024_regs(v, l);
+            quant_pair_store(v, e.hq + ((size_t)b * (HBLK / QK8) + (row >> 1)) * Q81_BYTES, row & 1);
+        }
+        __syncthreads();
+    }
+}
+
 // Workgroup of WAVES waves.  Each wave owns up to `units_per_wave` units
 // (grid-strided) and a private ring of D unit buffers in LDS; the workgroup shares one
 // LDS copy of the Q8_1 activation.  Every weight read is an LDS DMA
@@ -373,7 +474,7 @@ __device__ __forceinline__ double * rms_partials() {
 // same rows, only the lane's LDS offsets change (8-byte aligned code words,
 // no realignment).
 template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, bool GROUP = false, int NT = 1, bool RP = false,
-          bool RMS = false, bool OVL = false>
+          bool RMS = false, bool OVL = false, bool EPI = false>
 __global__ void __launch_bounds__(64 * WAVES)
 gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * __restrict__ signs,
                int32_t * __restrict__ dump, int units_per_wave, int n_tok, int xcd_log2m) {
@@ -385,6 +486,7 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
     static_assert(ROT == 0 || P::NCH % 32 == 0, "the rotation needs whole 1024-element blocks");
     static_assert(!RMS || ROT == 1 || ROT == 2, "RMSNorm rides on the fused rotation");
     static_assert(!OVL || (ROT == 1 && !RMS && !RP && NT == 1), "ring-staged rotation: plain FWHT");
+    static_assert(!EPI || (GROUP && NT == 1 && !DUMP && !RP), "FFN epilogue: the gate/up group");
     constexpr int ACT_BYTES = Q81_BYTES * P::NCH * NT;
     constexpr int NA = (ACT_BYTES + 1023) / 1024;          // activation DMA instructions
     constexpr int NHB = P::NCH / 32;                       // Hadamard blocks of the row
@@ -420,6 +522,12 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
     }
     const int NW = gridDim.x * WAVES;
     const int nu = gw < n_units ? min(units_per_wave, (n_units - 1 - gw) / NW + 1) : 0;
+    // EPI: the launch's generation, read at the start (its latency hides
+    // behind the first loads; only thread 0 of the workgroup uses it)
+    uint32_t epi_gen0 = 0;
+    if constexpr (EPI) {
+        if (threadIdx.x == 0) epi_gen0 = __hip_atomic_load(&mg.epi.sync[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 
     // OVL: the fp32 blocks are staged in the unit ring itself (the widest rows,
     // where a separate stage does not fit beside an 8-wave ring): slots k =
@@ -539,7 +647,7 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         if (nu > 0) wait_vmcnt<D * P::NPL>();
         else wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
-        if (nu <= 0) return;
+        if (nu <= 0 && !EPI) return;   // (EPI: every wave reaches the epilogue)
     } else if constexpr (OVL) {
         // 3. rotate and quantise the register blocks (a repeated one is rotated
         //    and not stored) while the first units stream in, then the barrier
@@ -555,7 +663,7 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);        // lgkmcnt(0): this wave's LDS stores are done
         __builtin_amdgcn_s_barrier();
-        if (nu <= 0) return;
+        if (nu <= 0 && !EPI) return;   // (EPI: every wave reaches the epilogue)
     } else {
         // 3. own staged blocks landed (all unit DMAs are younger); rotate and
         //    quantise them into the LDS activation (chunk c of block b at byte
@@ -606,7 +714,7 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);        // lgkmcnt(0): this wave's LDS stores are done
         __builtin_amdgcn_s_barrier();
-        if (nu <= 0) return;
+        if (nu <= 0 && !EPI) return;   // (EPI: every wave reaches the epilogue)
     }
 
     // the lane's chunk of slot j is the same in every unit: its activation
@@ -661,7 +769,7 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
     float ykeep = 0.0f;                       // lane (G i + r) NT + t keeps row r, token t of unit i
 
     int i = 0;
-    do {
+    if (nu > 0) do {
         const int slot = i % SL;
         const int newer = min(D - 1, nu - 1 - i);
         if (newer >= 2) wait_vmcnt<2 * P::NPL>();
@@ -736,11 +844,17 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         gs.at(gw + (rt / P::G) * NW, Wm, ym, n_out_m, lu);
         const int row = lu * P::G + rt % P::G;
         if (NT == 1) {
-            if (row < n_out_m) ym[row] = ykeep;
+            // EPI: other workgroups read these rows in this launch, so the
+            // store is coherent at device scope (written through to memory)
+            if (row < n_out_m) {
+                if constexpr (EPI) __hip_atomic_store(ym + row, ykeep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else ym[row] = ykeep;
+            }
         } else if (row < n_out_m && t < n_tok) {
             ym[(size_t)row * n_tok + t] = ykeep;
         }
     }
+    if constexpr (EPI) ffn_epilogue<WAVES>(mg, reinterpret_cast<float *>(&ring_all[0][0][0]), epi_gen0);
 }
 
 // Generic path: one wave per row, lane-strided chunks, 2-byte weight loads
@@ -857,7 +971,7 @@ bool group_units(MatGroup & mg, int n_mat) {
 }
 
 template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, int NT = 1, bool RP = false, bool RMS = false,
-          bool OVL = false>
+          bool OVL = false, bool EPI = false>
 int launch_nb_t(MatGroup mg, int n_mat, const void * xin, const float * signs, int32_t * dump,
                 int per_cu, hipStream_t st, int n_tok = 1) {
     using P = NbSpec<NB, NT>;
@@ -882,7 +996,12 @@ int launch_nb_t(MatGroup mg, int n_mat, const void * xin, const float * signs, i
     int xl = knob(pq2host::K_GEMV_XCD_LOG2M, 3);
     if (xl < 0 || xl > 3 || blocks % 8 != 0) xl = 0;
     while (xl > 0 && ((blocks / 8) * WAVES) % (1 << xl) != 0) --xl;
-    if constexpr (OVL) {
+    if constexpr (EPI) {
+        static_assert(!OVL && !RP && NT == 1 && !DUMP, "FFN epilogue: the fused gate/up group");
+        if (n_mat != 2) return 1;
+        hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, ROT, true, 1, false, RMS, false, true>),
+                           dim3(blocks), dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl);
+    } else if constexpr (OVL) {
         if (n_mat > 1)
             hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, ROT, true, 1, false, false, true>), dim3(blocks),
                                dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl);
@@ -1182,22 +1301,23 @@ int launch_nb_small_nt(const uint8_t * W, const uint8_t * X, float * Y, int n_ou
 // at 6144x5120 and 5120x6144, against 9.9 / 7.0 / 6.8 us for the pre-pass
 // plus the GEMV; two workgroups per CU: 6.9 us at 5120x6144), else 4 waves
 // with D = 2 or D = 1.  Returns -1 when no shape fits the LDS of a workgroup.
-template <int NB, int ROT, bool RP = false, bool RMS = false>
+template <int NB, int ROT, bool RP = false, bool RMS = false, bool EPI = false>
 int launch_nb_rot(const MatGroup & mg, int n_mat, const float * x, const float * signs, hipStream_t st) {
     const int waves = knob(pq2host::K_FGEMV_WAVES, 8);
     int per_cu = knob(pq2host::K_GEMV_WG_PER_CU, 0);
     if (per_cu <= 0) per_cu = 1;
     if constexpr (nb_lds_bytes<NB, 2, 8, ROT, 1, RMS>() <= LDS_PER_CU) {
-        if (waves == 8) return launch_nb_t<NB, 2, 8, false, ROT, 1, RP, RMS>(mg, n_mat, x, signs, nullptr, per_cu, st);
-    } else if constexpr (ROT == 1 && !RP && !RMS && nb_lds_bytes<NB, 2, 8, 1, 1, false, true>() <= LDS_PER_CU) {
+        if (waves == 8)
+            return launch_nb_t<NB, 2, 8, false, ROT, 1, RP, RMS, false, EPI>(mg, n_mat, x, signs, nullptr, per_cu, st);
+    } else if constexpr (ROT == 1 && !RP && !RMS && !EPI && nb_lds_bytes<NB, 2, 8, 1, 1, false, true>() <= LDS_PER_CU) {
         // the separate stage does not fit beside an 8-wave ring: stage in the ring
         if (waves == 8 && knob(pq2host::K_FGEMV_OVL, 1) == 1)
             return launch_nb_t<NB, 2, 8, false, 1, 1, false, false, true>(mg, n_mat, x, signs, nullptr, per_cu, st);
     }
     if constexpr (nb_lds_bytes<NB, 2, 4, ROT, 1, RMS>() <= LDS_PER_CU)
-        return launch_nb_t<NB, 2, 4, false, ROT, 1, RP, RMS>(mg, n_mat, x, signs, nullptr, per_cu, st);
+        return launch_nb_t<NB, 2, 4, false, ROT, 1, RP, RMS, false, EPI>(mg, n_mat, x, signs, nullptr, per_cu, st);
     else if constexpr (nb_lds_bytes<NB, 1, 4, ROT, 1, RMS>() <= LDS_PER_CU)
-        return launch_nb_t<NB, 1, 4, false, ROT, 1, RP, RMS>(mg, n_mat, x, signs, nullptr, per_cu, st);
+        return launch_nb_t<NB, 1, 4, false, ROT, 1, RP, RMS, false, EPI>(mg, n_mat, x, signs, nullptr, per_cu, st);
     else
         return -1;
 }
@@ -1462,6 +1582,66 @@ int gemv_repack_streaming(const void * W, const float * x, float * y, int64_t n_
     }
 }
 
+// FFN gate/up with the SwiGLU glue (bonsai_p40_ffn_gate_up_swiglu and its
+// allocation-free form): sync = two zeroed counters, gu = gate rows then up
+// rows (2 n_ff floats, 16-byte aligned).
+bool ffn_args_ok(const void * Wg, const void * Wu, const float * x, const void * hq, int64_t n_ff,
+                 int64_t n_embd) {
+    if (Wg == nullptr || Wu == nullptr || x == nullptr || hq == nullptr) return false;
+    if (n_ff <= 0 || n_ff % HBLK != 0 || n_ff > 0x3fffffff) return false;
+    if (n_embd <= 0 || n_embd % HBLK != 0 || n_embd / QK_PQ2 > (1 << 24)) return false;
+    return ((uintptr_t)hq & 3u) == 0;
+}
+
+int ffn_gate_up_swiglu(const void * Wg, const void * Wu, const float * x, const float * norm_w,
+                       const float * x_signs, const float * h_signs, void * hq, int64_t n_ff, int64_t n_embd,
+                       float eps, uint32_t * sync, float * gu, uint32_t * status, hipStream_t st) {
+    MatGroup mg{};
+    const void * Ws[2] = {Wg, Wu};
+    float * ys[2] = {gu, gu + n_ff};
+    const int64_t rows[2] = {n_ff, n_ff};
+    int64_t total = 0;
+    if (make_group(mg, Ws, ys, rows, 2, &total) != 0) return 1;
+    mg.norm_w = norm_w;
+    mg.eps = eps;
+    mg.epi.sync = sync;
+    mg.epi.h_signs = h_signs;
+    mg.epi.hq = static_cast<uint8_t *>(hq);
+    mg.epi.status = status;
+    mg.epi.nblk = (int)(n_ff / HBLK);
+    const bool al = group_w_aligned(mg, 2) && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)x_signs & 15u) == 0 &&
+                    ((uintptr_t)norm_w & 15u) == 0;
+    if (al && knob(pq2host::K_GEMV_KERNEL, 0) == 0) {
+        int rc = -1;
+        if (norm_w != nullptr) {
+#define PQ2_RMS_EPI_CASE(N)                                                                         \
+    case N: rc = x_signs ? launch_nb_rot<N, 2, false, true, true>(mg, 2, x, x_signs, st)            \
+                         : launch_nb_rot<N, 1, false, true, true>(mg, 2, x, x_signs, st); break;
+            switch (n_embd / QK_PQ2) {
+                PQ2_RMS_EPI_CASE(8) PQ2_RMS_EPI_CASE(40) PQ2_RMS_EPI_CASE(48)
+                default: break;
+            }
+#undef PQ2_RMS_EPI_CASE
+        } else {
+#define PQ2_ROT_EPI_CASE(N)                                                                         \
+    case N: rc = x_signs ? launch_nb_rot<N, 2, false, false, true>(mg, 2, x, x_signs, st)           \
+                         : launch_nb_rot<N, 1, false, false, true>(mg, 2, x, x_signs, st); break;
+            switch (n_embd / QK_PQ2) {
+                PQ2_ROT_EPI_CASE(8) PQ2_ROT_EPI_CASE(40) PQ2_ROT_EPI_CASE(48) PQ2_ROT_EPI_CASE(80)
+                PQ2_ROT_EPI_CASE(96) PQ2_ROT_EPI_CASE(136)
+                default: break;
+            }
+#undef PQ2_ROT_EPI_CASE
+        }
+        if (rc >= 0) return rc;
+    }
+    // other widths or alignments: the grouped fused GEMV, then the SwiGLU
+    // pre-pass (two launches, the same bytes)
+    const int rc = fwht_gemv_group_dispatch(mg, 2, x, x_signs, n_embd, st);
+    if (rc != 0) return rc;
+    return bonsai_p40_swiglu_fwht_quant(gu, gu + n_ff, h_signs, hq, n_ff, st);
+}
+
 }  // namespace pq2
 
 extern "C" {
@@ -1516,6 +1696,20 @@ int bonsai_p40_rmsnorm_fwht_gemv_group(const void * const * W, float * const * y
     mg.norm_w = norm_w;
     mg.eps = eps;
     return fwht_gemv_group_dispatch(mg, n_mat, x, signs, n_in, (hipStream_t)stream);
+}
+
+int bonsai_p40_ffn_gate_up_swiglu(const void * Wg, const void * Wu, const float * x, const float * norm_w,
+                                  const float * x_signs, const float * h_signs, void * hq, int64_t n_ff,
+                                  int64_t n_embd, float eps, void * workspace, uint32_t * status,
+                                  bonsai_stream stream) {
+    if (!pq2::ffn_args_ok(Wg, Wu, x, hq, n_ff, n_embd) || workspace == nullptr ||
+        ((uintptr_t)workspace & 15u) != 0)
+        return 1;
+    uint8_t * ws = static_cast<uint8_t *>(workspace);
+    return pq2::ffn_gate_up_swiglu(Wg, Wu, x, norm_w, x_signs, h_signs, hq, n_ff, n_embd, eps,
+                                   reinterpret_cast<uint32_t *>(ws),
+                                   reinterpret_cast<float *>(ws + BONSAI_P40_FFN_SYNC_BYTES), status,
+                                   (hipStream_t)stream);
 }
 
 int bonsai_p40_chunk_dots(const void * W, const void * xq, int32_t * out, int64_t n_out,

@@ -144,3 +144,22 @@ def test_concurrent_calls_from_host_threads():
     assert not errors
     assert len(out) == 8 * 40
     assert all(rc == serial[j] for j, rc in out)
+
+
+def test_ffn_gate_up_swiglu_argument_checks():
+    f = B.lib().bonsai_p40_ffn_gate_up_swiglu
+    args = [16, 16, 16, None, None, None, 16, 17408, 5120, C.c_float(1e-6)]
+    assert f(*args, None, None, None) == 1                      # no workspace
+    assert f(*args, 24, None, None) == 1                        # workspace not 16-byte aligned
+    bad = list(args)
+    bad[7] = 1000                                               # n_ff % 1024
+    assert f(*bad, 32, None, None) == 1
+    bad = list(args)
+    bad[8] = 5000                                               # n_embd % 1024
+    assert f(*bad, 32, None, None) == 1
+    bad = list(args)
+    bad[6] = 18                                                 # hq not 4-byte aligned
+    assert f(*bad, 32, None, None) == 1
+    bad = list(args)
+    bad[2] = None                                               # no x
+    assert f(*bad, 32, None, None) == 1
