@@ -216,6 +216,23 @@ int bonsai_p40_ffn_gate_up_swiglu(const void * Wg, const void * Wu, const float 
                                   int64_t n_embd, float eps, void * workspace, uint32_t * status,
                                   bonsai_stream stream);
 
+// bonsai_p40_ffn_gate_up_swiglu without a workspace argument, for callers
+// that cannot allocate device memory (code under HIP graph capture, tight
+// serving loops, harnesses that forbid allocation).  No counterpart in the
+// reference.  The workspace is a static device array inside the library of
+// BONSAI_P40_FFN_WORKSPACE_BYTES(BONSAI_P40_FFN_NOALLOC_MAX_NFF) bytes (~512
+// KiB), one per GPU for the life of the process; the call allocates nothing
+// (two kernel launches: a counter clear, then the fused launch).  Every call
+// on one GPU shares that array, so calls that overlap on one GPU (different
+// streams, different host threads) race and must not be issued.  Errors: as
+// bonsai_p40_ffn_gate_up_swiglu, plus 1 if n_ff > BONSAI_P40_FFN_NOALLOC_MAX_NFF;
+// the hipError_t of the one-time symbol lookup if it fails.
+#define BONSAI_P40_FFN_NOALLOC_MAX_NFF 65536
+int bonsai_p40_ffn_gate_up_swiglu_noalloc(const void * Wg, const void * Wu, const float * x,
+                                          const float * norm_w, const float * x_signs, const float * h_signs,
+                                          void * hq, int64_t n_ff, int64_t n_embd, float eps, uint32_t * status,
+                                          bonsai_stream stream);
+
 // Reference ternary weight quantiser: n fp32 weights (n % 128 == 0, rows of a
 // matrix back to back) -> n/128 block_pq2_0 with d = amax rounded to fp16
 // half away from zero and code = clamp(lroundf(x / amax) + 1, 0, 3); bytes

@@ -46,6 +46,8 @@ SIGNATURES = {
     "bonsai_p40_fwht_gemv_group": [_V, _V, _V, C.c_int, _F32P, _F32P, _I64, _V],
     "bonsai_p40_rmsnorm_fwht_gemv_group": [_V, _V, _V, C.c_int, _F32P, _F32P, _F32P, _I64, C.c_float, _V],
     "bonsai_p40_ffn_gate_up_swiglu": [_V, _V, _F32P, _F32P, _F32P, _F32P, _V, _I64, _I64, C.c_float, _V, _V, _V],
+    "bonsai_p40_ffn_gate_up_swiglu_noalloc": [_V, _V, _F32P, _F32P, _F32P, _F32P, _V, _I64, _I64, C.c_float,
+                                              _V, _V],
     "bonsai_p40_quantize_pq2_0": [_F32P, _V, _I64, _V],
     "bonsai_p40_dequantize_pq2_0": [_V, _F32P, _I64, _V],
     "bonsai_p40_chunk_dots": [_V, _V, _V, _I64, _I64, _V],
@@ -223,6 +225,19 @@ def ffn_gate_up_swiglu(Wg, Wu, x, norm_w, x_signs, h_signs, hq, n_ff: int, n_emb
     _check("bonsai_p40_ffn_gate_up_swiglu",
            call("bonsai_p40_ffn_gate_up_swiglu", Wg, Wu, x, norm_w, x_signs, h_signs, hq, n_ff, n_embd,
                 C.c_float(eps), workspace, status, stream=stream))
+
+
+FFN_NOALLOC_MAX_NFF = 65536
+
+
+def ffn_gate_up_swiglu_noalloc(Wg, Wu, x, norm_w, x_signs, h_signs, hq, n_ff: int, n_embd: int, eps: float,
+                               status=None, stream=None) -> None:
+    """ffn_gate_up_swiglu with the library's static per-GPU scratch instead of
+    a workspace (n_ff <= FFN_NOALLOC_MAX_NFF; calls on one GPU must not
+    overlap)."""
+    _check("bonsai_p40_ffn_gate_up_swiglu_noalloc",
+           call("bonsai_p40_ffn_gate_up_swiglu_noalloc", Wg, Wu, x, norm_w, x_signs, h_signs, hq, n_ff, n_embd,
+                C.c_float(eps), status, stream=stream))
 
 
 def quantize_pq2_0(x, w, n: int, stream=None) -> None:

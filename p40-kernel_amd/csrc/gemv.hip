@@ -1644,6 +1644,53 @@ int ffn_gate_up_swiglu(const void * Wg, const void * Wu, const float * x, const 
 
 }  // namespace pq2
 
+// ---------------------------------------------------------------------------
+// Allocation-free form of the FFN gate/up launch: its workspace is this
+// file-scope device array.  Each GPU the library runs on holds its own copy
+// until the process ends.  In host code `scratch` names a host-side stand-in,
+// not device memory: its device address comes from hipGetSymbolAddress, once
+// per device, and only that address is passed to kernels.
+namespace {
+
+constexpr int64_t FFN_NOALLOC_MAX_NFF = BONSAI_P40_FFN_NOALLOC_MAX_NFF;
+constexpr size_t FFN_SCRATCH_BYTES = (size_t)BONSAI_P40_FFN_WORKSPACE_BYTES(FFN_NOALLOC_MAX_NFF);
+
+__device__ __attribute__((aligned(256))) uint8_t scratch[FFN_SCRATCH_BYTES];
+
+// zeroes the ticket counter (the generation word may hold any value): a
+// kernel rather than a memset, so that a captured graph replays it correctly
+__global__ void __launch_bounds__(64) ffn_sync_clear_kernel(uint32_t * sync) {
+    if (threadIdx.x == 0) sync[0] = 0u;
+}
+
+struct ScratchAddr {
+    uint8_t * ptr = nullptr;
+    hipError_t err = hipSuccess;
+};
+
+// device address of `scratch` on the calling thread's current device, looked
+// up once per device with that device current
+ScratchAddr scratch_address() {
+    static pq2host::PerDeviceOnce once;
+    static ScratchAddr addr[pq2host::MAX_DEVICES];
+    const int d = pq2host::current_device();
+    if (d < 0 || d >= pq2host::MAX_DEVICES) {
+        ScratchAddr a;
+        a.err = hipErrorInvalidDevice;
+        return a;
+    }
+    pq2host::once_per_device(once, [d] {
+        void * p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) (void)hipGetLastError();
+        addr[d].err = e;
+        addr[d].ptr = e == hipSuccess ? static_cast<uint8_t *>(p) : nullptr;
+    });
+    return addr[d];
+}
+
+}  // namespace
+
 extern "C" {
 
 int bonsai_p40_gemv(const void * W, const void * xq, float * y, int64_t n_out, int64_t n_in,
@@ -1710,6 +1757,23 @@ int bonsai_p40_ffn_gate_up_swiglu(const void * Wg, const void * Wu, const float 
                                    reinterpret_cast<uint32_t *>(ws),
                                    reinterpret_cast<float *>(ws + BONSAI_P40_FFN_SYNC_BYTES), status,
                                    (hipStream_t)stream);
+}
+
+int bonsai_p40_ffn_gate_up_swiglu_noalloc(const void * Wg, const void * Wu, const float * x,
+                                          const float * norm_w, const float * x_signs, const float * h_signs,
+                                          void * hq, int64_t n_ff, int64_t n_embd, float eps, uint32_t * status,
+                                          bonsai_stream stream) {
+    if (!pq2::ffn_args_ok(Wg, Wu, x, hq, n_ff, n_embd)) return 1;
+    if (n_ff > FFN_NOALLOC_MAX_NFF) return 1;          // beyond the static scratch
+    const ScratchAddr a = scratch_address();
+    if (a.err != hipSuccess) return (int)a.err;
+    hipStream_t st = (hipStream_t)stream;
+    uint32_t * sync = reinterpret_cast<uint32_t *>(a.ptr);
+    hipLaunchKernelGGL(ffn_sync_clear_kernel, dim3(1), dim3(64), 0, st, sync);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    return pq2::ffn_gate_up_swiglu(Wg, Wu, x, norm_w, x_signs, h_signs, hq, n_ff, n_embd, eps, sync,
+                                   reinterpret_cast<float *>(a.ptr + BONSAI_P40_FFN_SYNC_BYTES), status, st);
 }
 
 int bonsai_p40_chunk_dots(const void * W, const void * xq, int32_t * out, int64_t n_out,
