@@ -1052,6 +1052,22 @@ int launch_nb(const MatGroup & mg, int n_mat, const uint8_t * xq, int32_t * dump
         for (int m = 0; m < n_mat; ++m) units += (mg.n_out[m] + NbSpec<NB, 1>::G - 1) / NbSpec<NB, 1>::G;
         const int64_t waves1 = 4 * (int64_t)cu_count();
         if (per_cu == 2 && units % waves1 == 0 && units / waves1 <= 3) per_cu = 1;
+        // rows of 5120 and 6144 columns (2-row units): other workgroup shapes
+        // measured faster on MI355X (same process, alternating shapes, us):
+        //   one 8-wave workgroup per CU: 17408x5120 6.95 -> 6.31, gate+up
+        //     grouped 11.08 -> 9.95, 5120x6144 4.11 -> 4.00;
+        //   one 6-wave workgroup per CU: q/k/v grouped (4096 units) 4.78 -> 4.62;
+        //   ring depth 1, three per CU: 1024x5120 (512 units) 2.91 -> 2.79;
+        //   6144x5120 (3 units per wave of one 4-wave workgroup per CU) and
+        //   the 17408-wide rows keep the shape above.
+        if constexpr (!DUMP && (NB == 40 || NB == 48)) {
+            if (NB == 48 || group_weight_bytes(mg, n_mat, NB) >= (16 << 20))
+                return launch_nb_t<NB, 2, 8, false>(mg, n_mat, xq, nullptr, dump, 1, st);
+            if (NB == 40 && units <= waves1)
+                return launch_nb_t<NB, 1, 4, false>(mg, n_mat, xq, nullptr, dump, 3, st);
+            if (NB == 40 && units > 3 * waves1)
+                return launch_nb_t<NB, 2, 6, false>(mg, n_mat, xq, nullptr, dump, 1, st);
+        }
     }
     return launch_nb_t<NB, 2, 4, DUMP>(mg, n_mat, xq, nullptr, dump, per_cu, st);
 }
