@@ -269,8 +269,32 @@ def bench_token_sweep(steps, warmup, gen, mode="separate"):
 
     nw = torch.randn(N_EMBD, generator=gen, device="cuda") * 0.1 + 1
     ws = torch.zeros(B.ffn_workspace_bytes(N_FF), dtype=torch.uint8, device="cuda")
+    chain = None
+    if mode == "chain":
+        # the whole token as one persistent launch: per layer q/k/v from the
+        # RMS-normalised layer input, o from q, gate/up from the normalised o,
+        # the SwiGLU glue, down; the next layer's input is this layer's down
+        # output (every step depends on the one before it)
+        yd = torch.empty(N_EMBD, device="cuda")
+        csteps = []
+        x_in = xs[N_EMBD]
+        for Wq, Wk, Wv, Wo, Wg, Wu, Wd in layers:
+            csteps += [
+                B.chain_step(B.CHAIN_RMSNORM_FWHT, [Wq, Wk, Wv], [ys[Q_DIM], yk, yv], [Q_DIM, KV_DIM, KV_DIM],
+                             N_EMBD, x=x_in, norm_w=nw, eps=1e-6),
+                B.chain_step(B.CHAIN_FWHT, [Wo], [ys[N_EMBD]], [N_EMBD], Q_DIM, x=ys[Q_DIM]),
+                B.chain_step(B.CHAIN_RMSNORM_FWHT, [Wg, Wu], [yg, yu], [N_FF, N_FF], N_EMBD, x=ys[N_EMBD],
+                             norm_w=nw, eps=1e-6),
+                B.chain_step(B.CHAIN_SWIGLU, n_in=N_FF, x=yg, x2=yu, q_out=qs[N_FF]),
+                B.chain_step(B.CHAIN_Q8, [Wd], [yd], [N_EMBD], N_FF, x=qs[N_FF]),
+            ]
+            x_in = yd
+        chain = B.Chain(csteps)
 
     def token(i):
+        if chain is not None:
+            chain.run()
+            return
         for L in layers:
             if mode == "layer_ffn":
                 Wq, Wk, Wv, Wo, Wg, Wu, Wd = L
@@ -306,6 +330,10 @@ def bench_token_sweep(steps, warmup, gen, mode="separate"):
                     B.gemv(W, qs[n_in], ys[n_out], n_out, n_in)
 
     ms = time_loop(token, steps, warmup, per_graph=1)
+    if chain is not None:
+        torch.cuda.synchronize()
+        if int(chain.status.item()) != 0:
+            raise RuntimeError("decode chain: a barrier wait gave up")
     del layers, proto
     return ms, wbytes
 
@@ -501,7 +529,7 @@ def main():
                     help="small-batch GEMM 17408x5120 with B tokens only (profiling)")
     ap.add_argument("--only-fused", action="store_true",
                     help="fused FWHT+Q8_1+GEMV 17408x5120 from fp32 only (profiling)")
-    ap.add_argument("--only-sweep", default="", metavar="MODE", choices=["", "separate", "fused", "grouped", "layer", "layer_ffn"],
+    ap.add_argument("--only-sweep", default="", metavar="MODE", choices=["", "separate", "fused", "grouped", "layer", "layer_ffn", "chain"],
                     help="config-2 token sweep in one mode only (profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -642,7 +670,10 @@ def main():
                            ("layer", "as grouped, with both layer RMSNorms inside the grouped launches "
                                      "and SwiGLU+FWHT+Q8_1 of the gate/up outputs feeding down"),
                            ("layer_ffn", "as layer, with the SwiGLU+FWHT+Q8_1 glue inside the gate/up launch "
-                                         "(bonsai_p40_ffn_gate_up_swiglu): 4 launches per layer")):
+                                         "(bonsai_p40_ffn_gate_up_swiglu): 4 launches per layer"),
+                           ("chain", "as layer, each step fed by the one before it, the whole token as ONE "
+                                     "persistent launch (bonsai_p40_chain_run: 320 steps, grid barriers, the next "
+                                     "step's weights prefetched through each barrier)")):
             m, wb = bench_token_sweep(5, 2, gen, mode=mode)
             extra[f"token_sweep_config2_{mode}"] = {"ms_per_token": round(m, 3), "tok/s": round(1e3 / m, 2),
                                                     "weight_GB/s": round(wb / (m * 1e-3) / 1e9, 1),

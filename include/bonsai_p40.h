@@ -245,6 +245,67 @@ int bonsai_p40_quantize_pq2_0(const float * x, void * w, int64_t n, bonsai_strea
 // Errors as bonsai_p40_quantize_pq2_0.
 int bonsai_p40_dequantize_pq2_0(const void * w, float * y, int64_t n, bonsai_stream stream);
 
+// ---------------------------------------------------------------------------
+// Decode chain: a sequence of dependent decode steps run by ONE persistent
+// launch (no counterpart in the reference, whose host launches every matmul
+// and glue op separately; each step computes exactly what the entry point
+// named beside its kind computes).  One workgroup per CU; between two steps
+// every workgroup waits at a grid-wide barrier (flag words in the workspace,
+// bounded polling), and while it waits its waves already stream the first
+// weight units of the next GEMV step into LDS.  A step's input may be an
+// earlier step's output.
+//   BONSAI_P40_CHAIN_Q8:     y[m] = W[m] . x, x the permuted Q8_1 of n_in
+//                            values (bonsai_p40_gemv_group);
+//   BONSAI_P40_CHAIN_FWHT:   x fp32: bonsai_p40_fwht_gemv_group (signs NULL or
+//                            length n_in);
+//   BONSAI_P40_CHAIN_RMSNORM_FWHT: x fp32: bonsai_p40_rmsnorm_fwht_gemv_group
+//                            with norm_w and eps;
+//   BONSAI_P40_CHAIN_SWIGLU: no matrix: q_out = Q8_1(FWHT(signs .* swiglu(x,
+//                            x2))) over n_in values (bonsai_p40_swiglu_fwht_quant).
+// Widths: FWHT / RMSNORM_FWHT n_in in {5120, 6144}; Q8 n_in in {5120, 6144,
+// 17408}; SWIGLU n_in % 1024 == 0.  Up to 4 matrices per step (16-byte
+// aligned, < 2 GiB each); x, x2, norm_w and signs 16-byte aligned, x of Q8
+// steps and q_out 4-byte aligned.
+#define BONSAI_P40_CHAIN_Q8 0
+#define BONSAI_P40_CHAIN_FWHT 1
+#define BONSAI_P40_CHAIN_RMSNORM_FWHT 2
+#define BONSAI_P40_CHAIN_SWIGLU 3
+typedef struct bonsai_p40_chain_step {
+    int kind;
+    int n_mat;                  // 1..4 (0 for SWIGLU)
+    const void * W[4];
+    float * y[4];
+    int64_t n_out[4];
+    int64_t n_in;
+    const void * x;             // input (Q8_1 bytes or fp32; SWIGLU: gate rows)
+    const float * x2;           // SWIGLU: up rows
+    const float * norm_w;       // RMSNORM_FWHT: n_in weights
+    const float * signs;        // NULL or n_in values of +-1
+    void * q_out;               // SWIGLU: Q8_1 output (n_in/32 blocks)
+    float eps;                  // RMSNORM_FWHT
+} bonsai_p40_chain_step;
+// Bytes of device memory a plan of n_steps steps needs.
+int64_t bonsai_p40_chain_plan_bytes(int n_steps);
+// Checks every step and writes the device form of the chain into plan (device
+// memory of bonsai_p40_chain_plan_bytes bytes) with a blocking copy: a set-up
+// call, made once per chain and device, before any launch that uses the plan
+// (and outside stream capture).  Errors: 1 if a step is invalid (nothing is
+// written), else the copy's hipError_t.
+int bonsai_p40_chain_plan(const bonsai_p40_chain_step * steps, int n_steps, void * plan);
+// Workspace of bonsai_p40_chain_run: one flag word per workgroup.  Zero-fill
+// it once before its first use and then leave it alone: every completed
+// launch leaves it ready for the next.  Launches that may run at the same time
+// need their own workspaces.
+#define BONSAI_P40_CHAIN_WORKSPACE_BYTES 4096
+// Runs a planned chain on the device it was planned on.  status (device, may
+// be NULL): incremented once for every barrier wait that gave up (the chain's
+// workgroups could not all be resident, e.g. beside another kernel); the
+// outputs of such a launch are not valid and the workspace must be
+// zero-filled again.  Errors: 1 on bad arguments, else the launch's
+// hipError_t.
+int bonsai_p40_chain_run(const void * plan, int n_steps, void * workspace, uint32_t * status,
+                         bonsai_stream stream);
+
 // Test hook: out[r * (n_in/32) + c] = the int32 chunk dot sum_k (code-1)*q of
 // row r, chunk c, computed by the same device code path as bonsai_p40_gemv
 // (the value of src/pq2_0.h:149-177 before scaling).  Errors as bonsai_p40_gemv.

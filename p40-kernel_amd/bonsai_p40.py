@@ -54,7 +54,11 @@ SIGNATURES = {
     "bonsai_p40_stream_read": [_V, _I64, _V, C.c_int, _V],
     "bonsai_p40_reload_tuning": [],
     "bonsai_p40_mfma_probe": [C.c_int, C.c_int, C.c_int, _V, _V, _V],
+    "bonsai_p40_chain_plan_bytes": [C.c_int],
+    "bonsai_p40_chain_plan": [_V, C.c_int, _V],
+    "bonsai_p40_chain_run": [_V, C.c_int, _V, _V, _V],
 }
+RESTYPES = {"bonsai_p40_chain_plan_bytes": C.c_int64}
 
 _lib = None
 
@@ -71,7 +75,7 @@ def lib() -> C.CDLL:
         for name, argtypes in SIGNATURES.items():
             fn = getattr(L, name)
             fn.argtypes = argtypes
-            fn.restype = C.c_int
+            fn.restype = RESTYPES.get(name, C.c_int)
         _lib = L
     return _lib
 
@@ -274,3 +278,64 @@ def pq2_bytes(n_out: int, n_in: int) -> int:
 
 def q8_bytes(n: int, n_tok: int = 1) -> int:
     return n // QK8 * n_tok * Q81_BYTES
+
+
+# ------------------------------------------------------------ decode chain
+CHAIN_Q8, CHAIN_FWHT, CHAIN_RMSNORM_FWHT, CHAIN_SWIGLU = 0, 1, 2, 3
+CHAIN_WORKSPACE_BYTES = 4096
+
+
+class ChainStep(C.Structure):
+    """bonsai_p40_chain_step of include/bonsai_p40.h."""
+    _fields_ = [("kind", C.c_int), ("n_mat", C.c_int), ("W", C.c_void_p * 4), ("y", C.c_void_p * 4),
+                ("n_out", C.c_int64 * 4), ("n_in", C.c_int64), ("x", C.c_void_p), ("x2", C.c_void_p),
+                ("norm_w", C.c_void_p), ("signs", C.c_void_p), ("q_out", C.c_void_p), ("eps", C.c_float)]
+
+
+def chain_step(kind: int, W=(), y=(), n_out=(), n_in: int = 0, x=None, x2=None, norm_w=None, signs=None,
+               q_out=None, eps: float = 0.0) -> ChainStep:
+    """One step of a decode chain; tensors are kept by pointer (the caller
+    keeps them alive while the plan is used)."""
+    s = ChainStep()
+    s.kind = kind
+    s.n_mat = len(W)
+    for i, (w, yy, n) in enumerate(zip(W, y, n_out)):
+        s.W[i] = _ptr(w)
+        s.y[i] = _ptr(yy)
+        s.n_out[i] = int(n)
+    s.n_in = int(n_in)
+    s.x, s.x2, s.norm_w, s.signs, s.q_out = (_ptr(t) for t in (x, x2, norm_w, signs, q_out))
+    s.eps = float(eps)
+    return s
+
+
+def chain_plan_bytes(n_steps: int) -> int:
+    return int(lib().bonsai_p40_chain_plan_bytes(n_steps))
+
+
+def chain_plan(steps, plan) -> None:
+    """Check the steps and write the device plan into `plan` (a device
+    tensor of chain_plan_bytes(len(steps)) bytes).  Blocking."""
+    arr = (ChainStep * len(steps))(*steps)
+    _check("bonsai_p40_chain_plan", lib().bonsai_p40_chain_plan(C.cast(arr, C.c_void_p), len(steps), _ptr(plan)))
+
+
+def chain_run(plan, n_steps: int, workspace, status=None, stream=None) -> None:
+    _check("bonsai_p40_chain_run",
+           call("bonsai_p40_chain_run", plan, n_steps, workspace, status, stream=stream))
+
+
+class Chain:
+    """A planned decode chain with its own plan buffer and workspace."""
+
+    def __init__(self, steps):
+        import torch
+        self.steps = list(steps)
+        self.n = len(self.steps)
+        self.plan = torch.empty(chain_plan_bytes(self.n), dtype=torch.uint8, device="cuda")
+        self.workspace = torch.zeros(CHAIN_WORKSPACE_BYTES, dtype=torch.uint8, device="cuda")
+        self.status = torch.zeros(1, dtype=torch.int32, device="cuda")
+        chain_plan(self.steps, self.plan)
+
+    def run(self, stream=None) -> None:
+        chain_run(self.plan, self.n, self.workspace, self.status, stream=stream)

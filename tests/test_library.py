@@ -14,7 +14,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def header_symbols():
     text = open(os.path.join(ROOT, "include", "bonsai_p40.h")).read()
-    return sorted(set(re.findall(r"^int\s+(bonsai_p40_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^(?:int|int64_t)\s+(bonsai_p40_\w+)\s*\(", text, re.M)))
 
 
 def test_library_exports_every_header_symbol():
@@ -163,3 +163,37 @@ def test_ffn_gate_up_swiglu_argument_checks():
     bad = list(args)
     bad[2] = None                                               # no x
     assert f(*bad, 32, None, None) == 1
+
+
+def test_chain_plan_argument_checks():
+    """Invalid decode-chain steps are rejected (rc 1) before anything touches
+    a device; the run entry point checks its pointers."""
+    L = B.lib()
+    ok = dict(W=[16], y=[16], n_out=[64], n_in=5120, x=16)
+    bad_steps = [
+        B.chain_step(7, **ok),                                              # unknown kind
+        B.chain_step(B.CHAIN_Q8, W=[16], y=[16], n_out=[64], n_in=5000, x=16),   # n_in % 1024
+        B.chain_step(B.CHAIN_Q8, W=[16], y=[16], n_out=[64], n_in=7168, x=16),   # width not supported
+        B.chain_step(B.CHAIN_FWHT, W=[16], y=[16], n_out=[64], n_in=17408, x=16),  # fused prologue at 17408
+        B.chain_step(B.CHAIN_Q8, W=[24], y=[16], n_out=[64], n_in=5120, x=16),   # W not 16-byte aligned
+        B.chain_step(B.CHAIN_FWHT, W=[16], y=[16], n_out=[64], n_in=5120, x=20),  # fp32 x not 16-byte aligned
+        B.chain_step(B.CHAIN_Q8, W=[16], y=[16], n_out=[0], n_in=5120, x=16),    # empty matrix
+        B.chain_step(B.CHAIN_Q8, W=[], y=[], n_out=[], n_in=5120, x=16),         # no matrix
+        B.chain_step(B.CHAIN_Q8, W=[16] * 4, y=[16] * 4, n_out=[8] * 4, n_in=5120, x=None),  # no input
+        B.chain_step(B.CHAIN_RMSNORM_FWHT, **ok),                           # no norm weights
+        B.chain_step(B.CHAIN_SWIGLU, n_in=17408, x=16, x2=None, q_out=16),  # no up rows
+        B.chain_step(B.CHAIN_SWIGLU, n_in=17408, x=16, x2=16, q_out=18),    # q_out not 4-byte aligned
+    ]
+    for i, s in enumerate(bad_steps):
+        arr = (B.ChainStep * 1)(s)
+        assert L.bonsai_p40_chain_plan(C.cast(arr, C.c_void_p), 1, 256) == 1, i
+    arr = (B.ChainStep * 1)(B.chain_step(B.CHAIN_Q8, **ok))
+    assert L.bonsai_p40_chain_plan(None, 1, 256) == 1
+    assert L.bonsai_p40_chain_plan(C.cast(arr, C.c_void_p), 0, 256) == 1
+    assert L.bonsai_p40_chain_plan(C.cast(arr, C.c_void_p), 1, None) == 1
+    assert L.bonsai_p40_chain_plan(C.cast(arr, C.c_void_p), 1, 264) == 1     # plan not 16-byte aligned
+    assert L.bonsai_p40_chain_plan_bytes(0) == 0
+    assert L.bonsai_p40_chain_plan_bytes(3) > 0
+    assert L.bonsai_p40_chain_run(None, 1, 256, None, None) == 1
+    assert L.bonsai_p40_chain_run(256, 1, None, None, None) == 1
+    assert L.bonsai_p40_chain_run(256, 0, 256, None, None) == 1
