@@ -491,7 +491,7 @@ def kernel_source_hash():
     traffic figure measured on another build of them is not reported."""
     import hashlib
     h = hashlib.sha256()
-    for f in ("gemv.hip", "pq2_device.h", "fwht_device.h"):
+    for f in ("gemv.hip", "gemv_device.h", "pq2_device.h", "fwht_device.h"):
         with open(os.path.join(ROOT, "p40-kernel_amd", "csrc", f), "rb") as fh:
             h.update(fh.read())
     return h.hexdigest()[:16]
