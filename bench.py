@@ -486,6 +486,32 @@ def mfma_peak(kind: int, iters: int = 4096, per_cu: int = 4):
     return tops, tops * 1e12 / ops_per_clk / 1e6
 
 
+def valu_mfma_overlap(iters: int = 4096, per_cu: int = 4):
+    """bonsai_p40_overlap_probe at 4 waves per SIMD: ms for 4 f16 MFMAs per
+    iteration alone, 16 fp32 FMAs alone (4 per MFMA: the prefill GEMM's
+    rescale ratio), and both in one wave stream."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    blocks = per_cu * cus
+    sink = torch.zeros(blocks, dtype=torch.int32, device="cuda")
+    out = {}
+    for name, mode in (("mfma_only", 0), ("fma_only", 1), ("both", 2)):
+        B.overlap_probe(mode, 1, blocks, 64, sink)
+        torch.cuda.synchronize()
+        best = None
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            B.overlap_probe(mode, 1, blocks, iters, sink)
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1)
+            best = ms if best is None else min(best, ms)
+        out[name + "_us"] = round(best * 1e3, 2)
+    out["both_over_sum"] = round(out["both_us"] / (out["mfma_only_us"] + out["fma_only_us"]), 3)
+    out["both_over_max"] = round(out["both_us"] / max(out["mfma_only_us"], out["fma_only_us"]), 3)
+    return out
+
+
 def kernel_source_hash():
     """sha256 over the device sources that build the decode GEMV kernel: a
     traffic figure measured on another build of them is not reported."""
@@ -529,6 +555,8 @@ def main():
                     help="small-batch GEMM 17408x5120 with B tokens only (profiling)")
     ap.add_argument("--only-fused", action="store_true",
                     help="fused FWHT+Q8_1+GEMV 17408x5120 from fp32 only (profiling)")
+    ap.add_argument("--only-probes", action="store_true",
+                    help="MFMA peak and VALU/MFMA overlap probes only (profiling)")
     ap.add_argument("--only-sweep", default="", metavar="MODE", choices=["", "separate", "fused", "grouped", "layer", "layer_ffn", "chain"],
                     help="config-2 token sweep in one mode only (profiling)")
     args = ap.parse_args()
@@ -546,6 +574,11 @@ def main():
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
 
+    if args.only_probes:
+        for kind in (0, 1):
+            print(f"[bench] mfma peak kind {kind}: {mfma_peak(kind)}", flush=True)
+        print(f"[bench] valu/mfma overlap: {valu_mfma_overlap()}", flush=True)
+        return
     if args.only_read:
         ms = bench_stream_read(gemv_bytes(N_FF, N_EMBD), args.steps, args.warmup)
         print(f"[bench] stream_read 23750272 B: {ms * 1e3:.2f} us", file=sys.stderr, flush=True)
@@ -618,6 +651,10 @@ def main():
                 "16 waves per CU; implied clock = measured rate / (CUs x 4 SIMDs x the instruction's "
                 "documented MACs per cycle x 2)"}
     print(f"[bench] mfma peak: {extra['mfma_peak_probe']}", file=sys.stderr, flush=True)
+    extra["valu_mfma_overlap"] = dict(valu_mfma_overlap(), note=(
+        "4 independent v_mfma_f32_16x16x32_f16 and 16 independent fp32 FMAs per iteration per wave, "
+        "4 waves per SIMD: both_over_sum near 1 means the VALU and the matrix core take turns"))
+    print(f"[bench] valu/mfma overlap: {extra['valu_mfma_overlap']}", file=sys.stderr, flush=True)
     if not args.quick:
         for (n_out, n_in, tag) in ((N_EMBD, N_FF, "gemv_5120x17408"), (N_EMBD, N_EMBD, "gemv_5120x5120")):
             m = bench_gemv(n_out, n_in, args.steps, args.warmup, gen)

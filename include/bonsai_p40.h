@@ -337,6 +337,14 @@ int bonsai_p40_stream_read(const void * buf, int64_t bytes, uint32_t * out, int 
 int bonsai_p40_mfma_probe(int kind, int blocks, int iters, uint64_t * clk, uint32_t * sink,
                           bonsai_stream stream);
 
+// Measurement helper: does the VALU work while the matrix core does?
+// `blocks` workgroups of 4 waves; per iteration each wave issues 4 independent
+// v_mfma_f32_16x16x32_f16 (mode 0 or 2) and nf x 16 independent fp32 FMAs
+// (mode 1 or 2).  Time modes 0, 1 and 2 with events: mode 2 near the larger
+// of the other two means overlap, near their sum means the two pipes take
+// turns.  sink needs `blocks` words.  Errors: 1 on bad arguments.
+int bonsai_p40_overlap_probe(int mode, int nf, int blocks, int iters, uint32_t * sink, bonsai_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -7,7 +7,9 @@
 //  * MFMA peak: back-to-back independent int8 (v_mfma_i32_16x16x64_i8) or f16
 //    (v_mfma_f32_16x16x32_f16) matrix instructions, with each wave's shader
 //    clock and real-time counters read around its loop so the host can derive
-//    the clock the MFMAs ran at.
+//    the clock the MFMAs ran at;
+//  * VALU / MFMA overlap: the same MFMAs with and without independent fp32
+//    FMAs in the same wave stream.
 #include "pq2_device.h"
 #include "../../include/bonsai_p40.h"
 
@@ -92,7 +94,66 @@ mfma_probe_kernel(int iters, uint64_t * __restrict__ clk, uint32_t * __restrict_
     if (fold == 0x9e3779b9u) sink[blockIdx.x] = fold;   // keeps the MFMAs live
 }
 
+// VALU / MFMA overlap probe.  Per iteration a wave issues 4 independent
+// v_mfma_f32_16x16x32_f16 (MODE 0 or 2) and nf x 16 independent fp32 FMAs
+// (MODE 1 or 2): with nf = 1 that is 4 FMAs per MFMA, the ratio of the
+// prefill GEMM's per-chunk rescale.  Comparing the three modes' times shows
+// whether the matrix core and the VALU work at the same time for one wave
+// stream.  The MFMAs are inline asm so that the compiler keeps the four
+// accumulators in place (it otherwise shuffles equal-looking ones).
+template <int MODE>
+__global__ void __launch_bounds__(256)
+overlap_probe_kernel(int iters, int nf, uint32_t * __restrict__ sink) {
+    const int lane = threadIdx.x & 63;
+    v8h a, b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        a[i] = (_Float16)(0.001f * (float)(lane + i));
+        b[i] = (_Float16)(0.002f * (float)(lane - i));
+    }
+    v4f acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        acc[i] = (v4f){(float)(lane + i), (float)(lane * (i + 2)), (float)(lane ^ (i + 1)), (float)(3 * i - lane)};
+    float f[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) f[i] = 0.5f * (float)lane + (float)i;
+    const float sc = 1.0001f + 1e-6f * (float)lane, tc = 0.999f;
+    for (int it = 0; it < iters; ++it) {
+        if constexpr (MODE != 1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(acc[i]) : "v"(a), "v"(b));
+        }
+        if constexpr (MODE != 0) {
+            for (int r = 0; r < nf; ++r) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) f[i] = fmaf(f[i], sc, tc);
+            }
+        }
+    }
+    float z = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) z += acc[i][0] + acc[i][1] + acc[i][2] + acc[i][3];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) z += f[i];
+    if (z == 1234.5f) sink[blockIdx.x] = 1u;       // practically never: keeps the work live
+}
+
 }  // namespace
+
+// VALU / MFMA overlap probe: `blocks` workgroups of 4 waves, each wave
+// iters x (4 MFMAs if mode != 1, nf x 16 FMAs if mode != 0).  sink needs
+// `blocks` words.  Errors: 1 on bad arguments.
+extern "C" int bonsai_p40_overlap_probe(int mode, int nf, int blocks, int iters, uint32_t * sink,
+                                        bonsai_stream stream) {
+    if (blocks <= 0 || iters <= 0 || nf < 0 || nf > 16 || sink == nullptr || mode < 0 || mode > 2) return 1;
+    const hipStream_t st = (hipStream_t)stream;
+    if (mode == 0) hipLaunchKernelGGL(overlap_probe_kernel<0>, dim3((unsigned)blocks), dim3(256), 0, st, iters, nf, sink);
+    else if (mode == 1) hipLaunchKernelGGL(overlap_probe_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, st, iters, nf, sink);
+    else hipLaunchKernelGGL(overlap_probe_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, st, iters, nf, sink);
+    return (int)hipGetLastError();
+}
 
 // MFMA peak probe: `blocks` workgroups of 4 waves, each wave issuing iters *
 // 4 MFMAs of the chosen kind (0: int8 16x16x64, 1: f16 16x16x32).  clk needs
