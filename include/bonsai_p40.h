@@ -130,8 +130,9 @@ int bonsai_p40_quant_tokens(const float * X, const float * signs, void * Xq, int
 // token rows of n floats, one launch in place of bonsai_p40_rmsnorm followed by
 // bonsai_p40_fwht and bonsai_p40_quant_activations (elementwise_p40.cu:17-41,
 // 48-88 + gemv_p40.cu:168-196; RMSNorm as src/ops.h:13-22).  The sum of squares
-// is accumulated in fp64, so the scale can differ from the reference's
-// sequential fp32 sum by that sum's rounding; the rest is bit-identical to the
+// is accumulated in fp64 in one order shared by every normalising entry point
+// (whatever n_tok), so the scale can differ from the reference's sequential
+// fp32 sum by that sum's rounding; the rest is bit-identical to the
 // host FWHT and quantiser.  Output chunk-major (block (c, t) at c*n_tok + t: the
 // GEMM's Xq; for n_tok == 1 the GEMV's xq).  x, w and signs are [n_tok][n], [n]
 // and [n] (signs may be NULL).  Errors: 1 if n <= 0, n % 1024 != 0, x or w is
@@ -158,6 +159,18 @@ int bonsai_p40_swiglu_fwht_quant(const float * gate, const float * up, const flo
 int bonsai_p40_fwht_gemv(const void * W, const float * x, const float * signs, float * y,
                          int64_t n_out, int64_t n_in, bonsai_stream stream);
 
+// Decode GEMV from an fp32 activation that is already in the weights' basis:
+// y = W . Q8_1(x), one launch in place of bonsai_p40_quant_activations
+// followed by bonsai_p40_gemv -- the reference's ggml hook sequence
+// (integrations/prismml/bonsai-p40.diff:283-291), which needs a Q8_1 scratch
+// buffer; this needs none.  Every workgroup quantises x into its own LDS with
+// the quantiser's device code (host rounding); on the model widths with
+// 16-byte aligned W and x, y is bit-identical to the two-call sequence.
+// Errors: 1 if n_in <= 0, n_in % 1024 != 0, x is NULL, or (other widths) the
+// Q8_1 activation does not fit in LDS (n_in > 130048); 0 (no-op) if n_out <= 0.
+int bonsai_p40_quant_gemv(const void * W, const float * x, float * y, int64_t n_out, int64_t n_in,
+                          bonsai_stream stream);
+
 // Grouped decode GEMV: y[m] = W[m] . xq for the n_mat (1..4) matrices that
 // multiply one activation (q, k and v; gate and up), in one launch over the
 // concatenated rows (the reference launches one GEMV per matrix,
@@ -183,8 +196,8 @@ int bonsai_p40_fwht_gemv_group(const void * const * W, float * const * y, const 
 // bonsai_p40_quant_activations + one bonsai_p40_gemv per matrix
 // (elementwise_p40.cu:48-88, 17-41 + gemv_p40.cu:168-219).  Every workgroup
 // normalises, rotates and quantises x into its own LDS; the sum of squares is
-// fp64 in a fixed order, so y[m] equals bonsai_p40_rmsnorm_fwht_quant followed
-// by bonsai_p40_gemv_group.  x and norm_w have n_in floats; signs may be NULL.
+// fp64, added in the one order every normalising entry point uses, so y[m]
+// equals bonsai_p40_rmsnorm_fwht_quant followed by bonsai_p40_gemv_group.  x and norm_w have n_in floats; signs may be NULL.
 // Errors: as bonsai_p40_fwht_gemv_group, plus 1 if norm_w is NULL.
 int bonsai_p40_rmsnorm_fwht_gemv_group(const void * const * W, float * const * y, const int64_t * n_out,
                                        int n_mat, const float * x, const float * norm_w, const float * signs,

@@ -42,6 +42,9 @@ SIGNATURES = {
     "bonsai_p40_swiglu_fwht_quant": [_F32P, _F32P, _F32P, _V, _I64, _V],
     "bonsai_p40_rmsnorm_fwht_quant": [_F32P, _F32P, _F32P, _V, _I64, _I64, C.c_float, _V],
     "bonsai_p40_fwht_gemv": [_V, _F32P, _F32P, _F32P, _I64, _I64, _V],
+    "bonsai_p40_quant_gemv": [_V, _F32P, _F32P, _I64, _I64, _V],
+    "bonsai_p40_ggml_should_use": [C.c_int, C.c_int, _I64],
+    "bonsai_p40_ggml_mul_mat": [_V, _V, _V, _V, C.c_size_t, _V],
     "bonsai_p40_gemv_group": [_V, _V, _V, C.c_int, _V, _I64, _V],
     "bonsai_p40_fwht_gemv_group": [_V, _V, _V, C.c_int, _F32P, _F32P, _I64, _V],
     "bonsai_p40_rmsnorm_fwht_gemv_group": [_V, _V, _V, C.c_int, _F32P, _F32P, _F32P, _I64, C.c_float, _V],
@@ -170,6 +173,43 @@ def rmsnorm_fwht_quant(x, w, signs, xq, n: int, n_tok: int, eps: float, stream=N
     _check("bonsai_p40_rmsnorm_fwht_quant",
            call("bonsai_p40_rmsnorm_fwht_quant", x, w, signs, xq, n, n_tok, C.c_float(eps),
                 stream=stream))
+
+
+def quant_gemv(W, x, y, n_out: int, n_in: int, stream=None) -> None:
+    """y = W . Q8_1(x), one launch (no rotation, no Q8_1 buffer)."""
+    _check("bonsai_p40_quant_gemv", call("bonsai_p40_quant_gemv", W, x, y, n_out, n_in, stream=stream))
+
+
+class GgmlTensor(C.Structure):
+    """bonsai_ggml_tensor of include/bonsai_p40_ggml.h: the ggml_tensor fields
+    the ggml hook reads."""
+    _fields_ = [("type", C.c_int), ("ne", C.c_int64 * 4), ("nb", C.c_size_t * 4), ("data", C.c_void_p)]
+
+
+GGML_TYPE_F32, GGML_TYPE_PQ2_0 = 0, 142
+
+
+def ggml_tensor(type_: int, ne, nb, data) -> GgmlTensor:
+    """A tensor view: ne and nb of up to 4 dimensions (missing ne are 1, the
+    nb of a missing dimension is the size of the one below), data a tensor
+    or a device pointer."""
+    ne = list(ne) + [1] * (4 - len(ne))
+    nb = list(nb)
+    while len(nb) < 4:
+        nb.append(nb[-1] * ne[len(nb) - 1])
+    return GgmlTensor(type_, (C.c_int64 * 4)(*ne), (C.c_size_t * 4)(*nb), _ptr(data))
+
+
+def ggml_should_use(src0_type: int, device: int, ne11: int) -> bool:
+    return lib().bonsai_p40_ggml_should_use(src0_type, device, ne11) == 1
+
+
+def ggml_mul_mat(src0: GgmlTensor, src1: GgmlTensor, dst: GgmlTensor, scratch=None, scratch_bytes: int = 0,
+                 stream=None) -> bool:
+    """True when the hook enqueued dst = src0 . src1, False when the caller
+    keeps its stock path."""
+    return lib().bonsai_p40_ggml_mul_mat(C.byref(src0), C.byref(src1), C.byref(dst), _ptr(scratch),
+                                         scratch_bytes, _stream(stream)) == 1
 
 
 def fwht_gemv(W, x, signs, y, n_out: int, n_in: int, stream=None) -> None:

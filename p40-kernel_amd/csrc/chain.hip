@@ -88,7 +88,7 @@ struct Arena {
     static constexpr int SS = XS + NHB * HBLK * 4;
     static constexpr int NS = SS + NHB * HBLK * 4;
     static constexpr int PART = NS + NHB * HBLK * 4;
-    static constexpr int END_ROT = PART + 8 * CW;       // with the fused prologue
+    static constexpr int END_ROT = PART + 8 * NHB;      // with the fused prologue (one partial per block)
     static constexpr int END_Q8 = ACT + ACT_BYTES;      // Q8 input only
 };
 // every wave's outputs of a step pass through LDS to wave 0, and the glue's
@@ -284,20 +284,18 @@ __device__ int gemv_step(const ChainStep & st, const ChainStep * plan, int d, in
         const int row = fwht_row(lane);
         float rs = 1.0f;
         if constexpr (KIND == BONSAI_P40_CHAIN_RMSNORM_FWHT) {
-            double ss = 0.0;
-            for (int b = wave; b < A::NHB; b += CW) {
-                const float * xb = xst + HBLK * b + 16 * row;
+            // the order of rms_sumsq, as the per-launch kernels
+            static_assert(A::NHB <= RMS_GROUP, "one group of block partials");
+            const double tot = rms_sumsq(
+                A::NHB, reinterpret_cast<double *>(arena + A::PART), CW, wave, lane,
+                [&](int b, float (&v)[16]) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) ss += (double)xb[r] * (double)xb[r];
-            }
-            ss = wave_sum_f64(ss);
-            double * part = reinterpret_cast<double *>(arena + A::PART);
-            if (lane == 0) part[wave] = ss;
-            __builtin_amdgcn_s_waitcnt(0xC07F);
-            __builtin_amdgcn_s_barrier();
-            double tot = 0.0;
-#pragma unroll
-            for (int i = 0; i < CW; ++i) tot += part[i];
+                    for (int r = 0; r < 16; ++r) v[r] = xst[HBLK * b + 16 * row + r];
+                },
+                [] {
+                    __builtin_amdgcn_s_waitcnt(0xC07F);
+                    __builtin_amdgcn_s_barrier();
+                });
             rs = 1.0f / sqrtf((float)(tot / (double)(A::NHB * HBLK)) + st.eps);
         }
         for (int b = wave; b < A::NHB; b += CW) {

@@ -208,4 +208,41 @@ __device__ __forceinline__ void quant_pair_store(const float (&v)[16], uint8_t *
     }
 }
 
+// The one summation order of an RMSNorm sum of squares, shared by every
+// kernel that normalises a row (the pre-pass kernels, the fused GEMVs, the
+// chain), so that all of them compute the same fp64 total bit for bit:
+//  * block b's partial: lane l adds the squares of its 16 elements
+//    HBLK b + 16 fwht_row(l) + r, r = 0..15, in order (each square is exact in
+//    fp64), then wave_sum_f64 adds the 64 lane sums as a balanced tree in lane
+//    order;
+//  * the total adds the block partials in block order 0, 1, ..., nhb - 1.
+// nw waves call this together; wave w computes the partials of blocks w,
+// w + nw, ... of each group of up to RMS_GROUP blocks into red (LDS,
+// RMS_GROUP doubles), every thread then adds the group in block order.
+// load(b, v) delivers the lane's 16 elements of block b; sync() is a
+// workgroup barrier that also completes this thread's LDS stores.  Returns
+// the total in every thread.
+constexpr int RMS_GROUP = 64;
+template <class Load, class Sync>
+__device__ __forceinline__ double rms_sumsq(int nhb, double * red, int nw, int wave, int lane, Load load,
+                                           Sync sync) {
+    double tot = 0.0;
+    for (int g = 0; g < nhb; g += RMS_GROUP) {
+        const int nbg = nhb - g < RMS_GROUP ? nhb - g : RMS_GROUP;
+        for (int b = wave; b < nbg; b += nw) {
+            float v[16];
+            load(g + b, v);
+            double s = 0.0;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s += (double)v[r] * (double)v[r];
+            s = wave_sum_f64(s);
+            if (lane == 0) red[b] = s;
+        }
+        sync();
+        for (int b = 0; b < nbg; ++b) tot += red[b];
+        if (g + RMS_GROUP < nhb) sync();          // red is refilled by the next group
+    }
+    return tot;
+}
+
 }  // namespace pq2

@@ -93,18 +93,19 @@ quant_kernel(const float * __restrict__ x, uint8_t * __restrict__ q, int nchunk,
 // RMSNorm -> FWHT -> Q8_1 of token rows (src/ops.h:13-22, then the pre-pass
 // above).  Grid n_tok, one workgroup per token, nw = min(n / 1024, 16) waves;
 // wave w owns the Hadamard blocks w, w + nw, ...  The sum of squares is
-// accumulated in fp64 (every fp32 square is exact there, and the rounding of
-// the fp64 sum sits far below fp32's), so s = 1 / sqrtf((float)(ss / n) + eps)
-// does not depend on the reduction order; the reference's sequential fp32 sum
-// differs from it by that sum's own rounding.  Then y = (x * s) * w, the
-// signs, the register FWHT and the quantiser, as the pre-pass.  Output
+// accumulated in fp64 in the one order every normalising kernel uses
+// (rms_sumsq: per-block lane sums, a wave tree, blocks in order), so every
+// path computes the same s = 1 / sqrtf((float)(ss / n) + eps); the
+// reference's sequential fp32 sum differs from it by that sum's own rounding.
+// Then y = (x * s) * w, the signs, the register FWHT and the quantiser, as
+// the pre-pass.  Output
 // chunk-major (block (c, t) at c * n_tok + t; for one token the GEMV layout).
 template <bool VEC, bool SIGNS>
 __global__ void __launch_bounds__(1024)
 rms_rot_quant_kernel(const float * __restrict__ x, const float * __restrict__ w,
                      const float * __restrict__ signs, uint8_t * __restrict__ q, int n, int n_tok,
                      float eps) {
-    __shared__ double red[16];
+    __shared__ double red[RMS_GROUP];
     const int l = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int tok = blockIdx.x;
@@ -112,18 +113,9 @@ rms_rot_quant_kernel(const float * __restrict__ x, const float * __restrict__ w,
     const int row = fwht_row(l);
     const float * xt = x + (size_t)tok * n;
 
-    double ss = 0.0;
-    for (int b = wave; b < nhb; b += nw) {
-        float v[16];
-        load16(xt + (size_t)HBLK * b + 16 * row, v, VEC);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) ss += (double)v[r] * (double)v[r];
-    }
-    ss = wave_sum_f64(ss);
-    if (l == 0) red[wave] = ss;
-    __syncthreads();
-    double tot = 0.0;
-    for (int i = 0; i < nw; ++i) tot += red[i];
+    const double tot = rms_sumsq(
+        nhb, red, nw, wave, l, [&](int b, float (&v)[16]) { load16(xt + (size_t)HBLK * b + 16 * row, v, VEC); },
+        [] { __syncthreads(); });
     const float s = 1.0f / sqrtf((float)(tot / (double)n) + eps);
 
     for (int b = wave; b < nhb; b += nw) {
@@ -145,9 +137,9 @@ rms_rot_quant_kernel(const float * __restrict__ x, const float * __restrict__ w,
 }
 
 // The same, one workgroup (4 waves) per (Hadamard block, token) for few
-// tokens: every workgroup computes the token's sum of squares itself, with
-// the same code and the same thread-to-element order (so all blocks of a
-// token get a bit-identical scale), while wave 0's own block of x, w and
+// tokens: every workgroup computes the token's sum of squares itself, in the
+// order of rms_sumsq (so all blocks of a token, and every other normalising
+// kernel, get a bit-identical scale), while wave 0's own block of x, w and
 // signs is already in flight; wave 0 then normalises, rotates and quantises.
 // The whole row is read once per block (an L2 hit after the first): the
 // blocks spread over the CUs instead of queueing on one.
@@ -156,7 +148,7 @@ __global__ void __launch_bounds__(256)
 rms_rot_quant_block_kernel(const float * __restrict__ x, const float * __restrict__ w,
                            const float * __restrict__ signs, uint8_t * __restrict__ q, int n,
                            int n_tok, float eps) {
-    __shared__ double red[4];
+    __shared__ double red[RMS_GROUP];
     const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
     const int b = blockIdx.x, tok = blockIdx.y;
     const int row = fwht_row(l);
@@ -167,22 +159,11 @@ rms_rot_quant_block_kernel(const float * __restrict__ x, const float * __restric
         load16(w + (size_t)HBLK * b + 16 * row, wv, VEC);
         if constexpr (SIGNS) load16(signs + (size_t)HBLK * b + 16 * row, sg, VEC);
     }
-    double ss = 0.0;
-    if constexpr (VEC) {
-        const float4 * x4 = reinterpret_cast<const float4 *>(xt);
-        for (int i = tid; i < n / 4; i += 256) {
-            const float4 t = x4[i];
-            ss += (double)t.x * (double)t.x + (double)t.y * (double)t.y;
-            ss += (double)t.z * (double)t.z + (double)t.w * (double)t.w;
-        }
-    } else {
-        for (int i = tid; i < n; i += 256) ss += (double)xt[i] * (double)xt[i];
-    }
-    ss = wave_sum_f64(ss);
-    if (l == 0) red[wave] = ss;
-    __syncthreads();
+    const double tot = rms_sumsq(
+        n / HBLK, red, 4, wave, l,
+        [&](int bb, float (&u)[16]) { load16(xt + (size_t)HBLK * bb + 16 * row, u, VEC); },
+        [] { __syncthreads(); });
     if (wave != 0) return;
-    const double tot = (red[0] + red[1]) + (red[2] + red[3]);
     const float s = 1.0f / sqrtf((float)(tot / (double)n) + eps);
 #pragma unroll
     for (int r = 0; r < 16; ++r) v[r] = v[r] * s * wv[r];

@@ -564,25 +564,23 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         if (nu > 0) wait_vmcnt<D * P::NPL>();
         else wait_vmcnt<0>();
         const int row = fwht_row(lane);
-        // RMSNorm scale: each wave sums the squares of its own blocks in fp64
-        // (exact squares), the partials meet in LDS in wave order -- the same
-        // order in every workgroup, so all of them use the same scale
+        // RMSNorm scale: the fp64 sum of squares in the order of rms_sumsq
+        // (block partials of the waves, added in block order), the same in
+        // every workgroup and in every other normalising kernel
         float rs = 1.0f;
         if constexpr (RMS) {
-            double ss = 0.0;
-            for (int b = wave; b < NHB; b += WAVES) {
-                const float * xb = rot_x_stage<NHB * HBLK>() + HBLK * b + 16 * row;
+            static_assert(NHB <= RMS_GROUP, "one group of block partials");
+            const float * xst = rot_x_stage<NHB * HBLK>();
+            const double tot = rms_sumsq(
+                NHB, rms_partials<NHB>(), WAVES, wave, lane,
+                [&](int b, float (&v)[16]) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) ss += (double)xb[r] * (double)xb[r];
-            }
-            ss = wave_sum_f64(ss);
-            double * part = rms_partials<WAVES>();
-            if (lane == 0) part[wave] = ss;
-            __builtin_amdgcn_s_waitcnt(0xC07F);
-            __builtin_amdgcn_s_barrier();
-            double tot = 0.0;
-#pragma unroll
-            for (int i = 0; i < WAVES; ++i) tot += part[i];
+                    for (int r = 0; r < 16; ++r) v[r] = xst[HBLK * b + 16 * row + r];
+                },
+                [] {   // LDS only: the unit DMAs stay in flight
+                    __builtin_amdgcn_s_waitcnt(0xC07F);
+                    __builtin_amdgcn_s_barrier();
+                });
             rs = 1.0f / sqrtf((float)(tot / (double)(NHB * HBLK)) + mg.eps);
         }
         for (int b = wave; b < NHB; b += WAVES) {
@@ -844,7 +842,7 @@ constexpr int nb_lds_bytes() {
     constexpr int ring = WAVES * (D + 1) * P::LDSB;
     constexpr int nhb = P::NCH / 32;
     constexpr int stage = OVL ? 0 : (ROT ? nhb * HBLK * 4 : 0) + (ROT == 2 ? nhb * HBLK * 4 : 0)   // ROT 3: x only
-                          + (RMS ? nhb * HBLK * 4 + 8 * WAVES : 0);
+                          + (RMS ? nhb * HBLK * 4 + 8 * nhb : 0);
     return act + ring + stage;
 }
 
@@ -1232,17 +1230,19 @@ int launch_nb_rot(const MatGroup & mg, int n_mat, const float * x, const float *
 }
 
 // Generic fused path (any n_in % 1024 == 0 whose Q8_1 activation fits in
-// LDS): every workgroup rotates and quantises the whole activation into LDS
-// (one Hadamard block per wave at a time), then each wave computes one row
+// LDS): every workgroup rotates (unless rotate is false) and quantises the
+// whole activation into LDS (one Hadamard block per wave at a time), then each
+// wave computes one row
 // with the lane-strided chunk walk of gemv_rowwave_kernel.  With norm_w, x is
 // first RMS-normalised: the workgroup sums the squares of all of x in fp64 in
-// a fixed thread order (the same in every workgroup).
+// the order of rms_sumsq (the same in every workgroup and every other
+// normalising kernel).
 __global__ void __launch_bounds__(GV_THREADS)
 gemv_rot_generic_kernel(const uint8_t * __restrict__ W, const float * __restrict__ x,
                         const float * __restrict__ signs, float * __restrict__ y, int n_out, int nb,
-                        bool vec, const float * __restrict__ norm_w, float eps) {
+                        bool vec, const float * __restrict__ norm_w, float eps, bool rotate) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ double red[GV_WAVES];
+    __shared__ double red[RMS_GROUP];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nchunk = 4 * nb;
@@ -1250,13 +1250,10 @@ gemv_rot_generic_kernel(const uint8_t * __restrict__ W, const float * __restrict
     const int xrow = fwht_row(lane);
     float rs = 1.0f;
     if (norm_w != nullptr) {
-        double ss = 0.0;
-        for (int i = threadIdx.x; i < 32 * nchunk; i += GV_THREADS) ss += (double)x[i] * (double)x[i];
-        ss = wave_sum_f64(ss);
-        if (lane == 0) red[wave] = ss;
-        __syncthreads();
-        double tot = 0.0;
-        for (int i = 0; i < GV_WAVES; ++i) tot += red[i];
+        const double tot = rms_sumsq(
+            nchunk / 32, red, GV_WAVES, wave, lane,
+            [&](int b, float (&v)[16]) { load16(x + (size_t)HBLK * b + 16 * xrow, v, vec); },
+            [] { __syncthreads(); });
         rs = 1.0f / sqrtf((float)(tot / (double)(32 * nchunk)) + eps);
     }
     for (int b = wave; b < nchunk / 32; b += GV_WAVES) {
@@ -1276,7 +1273,7 @@ gemv_rot_generic_kernel(const uint8_t * __restrict__ W, const float * __restrict
 #pragma unroll
             for (int r = 0; r < 16; ++r) v[r] *= sg[r];
         }
-        fwht1024_regs(v, lane);
+        if (rotate) fwht1024_regs(v, lane);
         quant_pair_store(v, act + (size_t)Q81_BYTES * (32 * b + (xrow >> 1)), xrow & 1);
     }
     __syncthreads();
@@ -1307,6 +1304,53 @@ bool group_w_aligned(const MatGroup & mg, int n_mat) {
     for (int m = 0; m < n_mat; ++m)
         if (((uintptr_t)mg.W[m] & 15u) != 0) return false;
     return true;
+}
+
+// One generic fused launch per matrix of a group (rotate = false: Q8_1 of x
+// itself); 1 when the activation does not fit in a workgroup's LDS.
+int rot_generic_launch(const MatGroup & mg, int n_mat, const float * x, const float * signs, int64_t n_in,
+                       bool rotate, hipStream_t st) {
+    const size_t lds = rot_generic_lds(n_in);
+    if (lds > (size_t)max_lds_per_block()) return 1;
+    // the kernel's static LDS (its fp64 partial sums) comes off the maximum
+    static pq2host::PerDeviceOnce attr;
+    pq2host::once_per_device(attr, [] {
+        pq2host::set_max_dynamic_lds(reinterpret_cast<const void *>(gemv_rot_generic_kernel),
+                                     max_lds_per_block() - 1024);
+    });
+    if (lds > (size_t)max_lds_per_block() - 1024) return 1;
+    const bool vec = ((uintptr_t)x & 15u) == 0 && ((uintptr_t)signs & 15u) == 0 &&
+                     ((uintptr_t)mg.norm_w & 15u) == 0;
+    for (int m = 0; m < n_mat; ++m) {
+        if (mg.n_out[m] <= 0) continue;
+        const unsigned blocks = (unsigned)((mg.n_out[m] + GV_WAVES - 1) / GV_WAVES);
+        hipLaunchKernelGGL(gemv_rot_generic_kernel, dim3(blocks), dim3(GV_THREADS), lds, st, mg.W[m], x,
+                           signs, mg.y[m], mg.n_out[m], (int)(n_in / QK_PQ2), vec, mg.norm_w, mg.eps, rotate);
+        const int rc = (int)hipGetLastError();
+        if (rc != 0) return rc;
+    }
+    return 0;
+}
+
+// Q8_1 (no rotation) + GEMV of one matrix in one launch: the streaming
+// kernel on the model widths (the activation quantised into every
+// workgroup's LDS, as the fused FWHT path without its butterflies), else the
+// generic fused kernel.
+int quant_gemv_dispatch(const MatGroup & mg, const float * x, int64_t n_in, hipStream_t st) {
+    if (group_w_aligned(mg, 1) && ((uintptr_t)x & 15u) == 0 && knob(pq2host::K_GEMV_KERNEL, 0) == 0) {
+        int rc = -1;
+        switch (n_in / QK_PQ2) {
+            case 8: rc = launch_nb_rot<8, 3>(mg, 1, x, nullptr, st); break;
+            case 40: rc = launch_nb_rot<40, 3>(mg, 1, x, nullptr, st); break;
+            case 48: rc = launch_nb_rot<48, 3>(mg, 1, x, nullptr, st); break;
+            case 80: rc = launch_nb_rot<80, 3>(mg, 1, x, nullptr, st); break;
+            case 96: rc = launch_nb_rot<96, 3>(mg, 1, x, nullptr, st); break;
+            case 136: rc = launch_nb_rot<136, 3>(mg, 1, x, nullptr, st); break;
+            default: break;
+        }
+        if (rc >= 0) return rc;
+    }
+    return rot_generic_launch(mg, 1, x, nullptr, n_in, false, st);
 }
 
 // Fused FWHT + Q8_1 + GEMV of a group: one streaming launch on the model
@@ -1341,26 +1385,7 @@ int fwht_gemv_group_dispatch(const MatGroup & mg, int n_mat, const float * x, co
         }
         if (rc >= 0) return rc;
     }
-    const size_t lds = rot_generic_lds(n_in);
-    if (lds > (size_t)max_lds_per_block()) return 1;
-    // the kernel's static LDS (its fp64 partial sums) comes off the maximum
-    static pq2host::PerDeviceOnce attr;
-    pq2host::once_per_device(attr, [] {
-        pq2host::set_max_dynamic_lds(reinterpret_cast<const void *>(gemv_rot_generic_kernel),
-                                     max_lds_per_block() - 1024);
-    });
-    if (lds > (size_t)max_lds_per_block() - 1024) return 1;
-    const bool vec = ((uintptr_t)x & 15u) == 0 && ((uintptr_t)signs & 15u) == 0 &&
-                     ((uintptr_t)mg.norm_w & 15u) == 0;
-    for (int m = 0; m < n_mat; ++m) {
-        if (mg.n_out[m] <= 0) continue;
-        const unsigned blocks = (unsigned)((mg.n_out[m] + GV_WAVES - 1) / GV_WAVES);
-        hipLaunchKernelGGL(gemv_rot_generic_kernel, dim3(blocks), dim3(GV_THREADS), lds, st, mg.W[m], x,
-                           signs, mg.y[m], mg.n_out[m], (int)(n_in / QK_PQ2), vec, mg.norm_w, mg.eps);
-        const int rc = (int)hipGetLastError();
-        if (rc != 0) return rc;
-    }
-    return 0;
+    return rot_generic_launch(mg, n_mat, x, signs, n_in, true, st);
 }
 
 // One matrix on the widths without a specialised kernel: the runtime-shaped
@@ -1627,6 +1652,14 @@ int bonsai_p40_fwht_gemv(const void * W, const float * x, const float * signs, f
     if (n_out <= 0) return 0;
     if (n_out > 0x3fffffff || n_in / QK_PQ2 > (1 << 24)) return 1;
     return fwht_gemv_group_dispatch(single_group(W, y, n_out), 1, x, signs, n_in, (hipStream_t)stream);
+}
+
+int bonsai_p40_quant_gemv(const void * W, const float * x, float * y, int64_t n_out, int64_t n_in,
+                          bonsai_stream stream) {
+    if (n_in <= 0 || n_in % HBLK != 0 || x == nullptr) return 1;
+    if (n_out <= 0) return 0;
+    if (n_out > 0x3fffffff || n_in / QK_PQ2 > (1 << 24)) return 1;
+    return quant_gemv_dispatch(single_group(W, y, n_out), x, n_in, (hipStream_t)stream);
 }
 
 int bonsai_p40_fwht_gemv_group(const void * const * W, float * const * y, const int64_t * n_out, int n_mat,

@@ -2,8 +2,9 @@
 // concurrent callers on any number of devices.
 //
 //  * Tuning knobs (BONSAI_* environment variables, used by tests and sweeps to
-//    pick a kernel variant) are read once, on first use, into atomics; the
-//    launch paths then read integers, never the environment.
+//    pick a kernel variant, and the ggml hook's opt-in switches) are read
+//    once, on first use, into atomics; the launch paths then read integers,
+//    never the environment.
 //    bonsai_p40_reload_tuning() re-reads them (a test that changes a variable
 //    calls it).
 //  * Device properties (CU count, LDS per workgroup) are cached per device id,
@@ -41,6 +42,8 @@ enum Knob : int {
     K_GEMM_F16_BN,
     K_GEMM_F16_SPLIT,
     K_GEMM_F16_WAVES,
+    K_GGML_ENABLE,
+    K_GGML_VERBOSE,
     K_COUNT
 };
 
@@ -51,7 +54,8 @@ inline const char * knob_name(int k) {
         "BONSAI_MFMA4_MIN_TOK",       "BONSAI_FGEMV_WAVES",     "BONSAI_FGEMV_OVL",
         "BONSAI_GEMM_SMALL_GEMV",     "BONSAI_GEMM_BD",         "BONSAI_GEMM_SMALL",
         "BONSAI_GEMM_SMALL_CFG",      "BONSAI_GEMM_KERNEL",     "BONSAI_GEMM_F16_BN",
-        "BONSAI_GEMM_F16_SPLIT",      "BONSAI_GEMM_F16_WAVES",
+        "BONSAI_GEMM_F16_SPLIT",      "BONSAI_GEMM_F16_WAVES",  "BONSAI_P40",
+        "BONSAI_P40_VERBOSE",
     };
     return names[k];
 }

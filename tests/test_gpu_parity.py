@@ -774,12 +774,66 @@ def test_ffn_chain_config1():
 
 
 # ------------------------------------------- RMSNorm -> FWHT -> Q8_1 pre-pass
+FWHT_ROWS = np.array([(((l ^ (l >> 2)) & 1) | ((((l >> 1) ^ (l >> 2)) & 1) << 1) |
+                       ((((l >> 2) ^ (l >> 3)) & 1) << 2) | (l & 0x38)) for l in range(64)])
+
+
+def rms_sumsq_canonical(x: np.ndarray) -> float:
+    """The kernels' one summation order of the fp64 sum of squares: per
+    1024-block, lane l adds the (exact) squares of its 16 elements
+    16 row(l) + r in order, the 64 lane sums meet in a balanced tree in lane
+    order (the DPP moves and readlanes of the wave sum), and the block sums
+    are added in block order."""
+    tot = 0.0
+    for b in range(x.size // 1024):
+        lanes = x[1024 * b:1024 * (b + 1)].astype(np.float64).reshape(64, 16)[FWHT_ROWS]
+        s = np.zeros(64)
+        for r in range(16):
+            s = s + lanes[:, r] * lanes[:, r]
+        while s.size > 1:
+            s = s[0::2] + s[1::2]
+        tot = tot + s[0]
+    return tot
+
+
 def rms_scale_fp64(x: np.ndarray, eps: float) -> np.float32:
-    """The fused kernel's scale: fp64 sum of the (exact) squares, then
+    """The fused kernels' scale: the canonical fp64 sum of squares, then
     1 / sqrtf(float(ss / n) + eps) in fp32 (each step correctly rounded)."""
-    ss = np.sum(x.astype(np.float64) ** 2)
-    m = np.float32(ss / x.size)
+    m = np.float32(rms_sumsq_canonical(x) / x.size)
     return np.float32(1.0) / np.sqrt(np.float32(m + np.float32(eps)))
+
+
+def test_rms_sum_order_is_one_order():
+    """Every normalising path adds the squares in the same order, so they
+    agree byte for byte even on a row whose fp64 sum of squares depends on
+    the order (values over 24 decades): the per-block pre-pass (few
+    tokens), the per-token pre-pass (many tokens), the grouped GEMV with the
+    norm inside (its y equals the GEMV of the pre-pass output) and the
+    emulation of the canonical order."""
+    case("rms sum order: per-block, per-token, fused GEMV, n=5120")
+    n, eps = 5120, 1e-6
+    g = O.gen_normal(2900, n)
+    x = (g * np.power(10.0, (O.gen_normal(2901, n) * 4).clip(-12, 12))).astype(np.float32)
+    x64 = x.astype(np.float64) ** 2
+    assert np.sum(x64) != rms_sumsq_canonical(x) or np.sum(x64[::-1]) != rms_sumsq_canonical(x)
+    w = O.gen_normal(2902, n) * 0.1 + 1
+    xq1 = torch.zeros(n // 32 * 36, dtype=torch.uint8, device="cuda")
+    B.rmsnorm_fwht_quant(dev(x), dev(w), None, xq1, n, 1, eps)                 # per-block kernel
+    n_tok = 1000                                                               # per-token kernel
+    X = np.tile(x, (n_tok, 1))
+    xqn = torch.zeros(n // 32 * 36 * n_tok, dtype=torch.uint8, device="cuda")
+    B.rmsnorm_fwht_quant(dev(X), dev(w), None, xqn, n, n_tok, eps)
+    got_n = host(xqn).reshape(n // 32, n_tok, 36)[:, 0, :].reshape(-1)
+    s = rms_scale_fp64(x, eps)
+    exp = O.quantize_q8_1(O.fwht(((x * s).astype(np.float32) * w).astype(np.float32)), True)
+    np.testing.assert_array_equal(host(xq1), exp)
+    np.testing.assert_array_equal(got_n, exp)
+    W = O.gen_weights(2903, 1024, n)
+    y_fused = torch.zeros(1024, dtype=torch.float32, device="cuda")
+    B.rmsnorm_fwht_gemv_group([dev(W)], dev(x), dev(w), None, [y_fused], [1024], n, eps)
+    y_two = torch.zeros(1024, dtype=torch.float32, device="cuda")
+    B.gemv_group([dev(W)], xq1, [y_two], [1024], n)
+    np.testing.assert_array_equal(host(y_fused).view(np.uint32), host(y_two).view(np.uint32))
 
 
 def chunk_major(blocks):

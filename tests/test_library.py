@@ -12,9 +12,16 @@ import bonsai_p40 as B
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def header_symbols():
-    text = open(os.path.join(ROOT, "include", "bonsai_p40.h")).read()
+def header_symbols(headers=("bonsai_p40.h", "bonsai_p40_ggml.h")):
+    text = "".join(open(os.path.join(ROOT, "include", h)).read() for h in headers)
     return sorted(set(re.findall(r"^(?:int|int64_t)\s+(bonsai_p40_\w+)\s*\(", text, re.M)))
+
+
+def test_every_header_is_scanned():
+    """The export check covers every header of include/ that declares entry points."""
+    for h in os.listdir(os.path.join(ROOT, "include")):
+        found = header_symbols((h,))
+        assert not found or h in ("bonsai_p40.h", "bonsai_p40_ggml.h"), h
 
 
 def test_library_exports_every_header_symbol():
@@ -30,7 +37,7 @@ def test_reference_symbol_set_is_kept():
     ref = ["bonsai_p40_gemv", "bonsai_p40_quant_activations", "bonsai_p40_gemm",
            "bonsai_p40_repack", "bonsai_p40_gemv_repack", "bonsai_p40_fwht",
            "bonsai_p40_rmsnorm", "bonsai_p40_gdn_step", "bonsai_p40_attn"]
-    assert set(ref) <= set(header_symbols())
+    assert set(ref) <= set(header_symbols(("bonsai_p40.h",)))
 
 
 NULL = None
@@ -59,6 +66,9 @@ NULL = None
     ("bonsai_p40_fwht_gemv", (NULL, 16, NULL, NULL, 16, 1000), 1),    # n_in % 1024
     ("bonsai_p40_fwht_gemv", (NULL, NULL, NULL, NULL, 16, 1024), 1),  # x NULL
     ("bonsai_p40_fwht_gemv", (NULL, 16, NULL, NULL, 0, 1024), 0),     # empty no-op
+    ("bonsai_p40_quant_gemv", (NULL, 16, NULL, 16, 1000), 1),          # n_in % 1024
+    ("bonsai_p40_quant_gemv", (NULL, NULL, NULL, 16, 1024), 1),        # x NULL
+    ("bonsai_p40_quant_gemv", (NULL, 16, NULL, 0, 1024), 0),           # empty no-op
     ("bonsai_p40_gemv_group", (NULL, NULL, NULL, 1, NULL, 128), 1),   # NULL arrays
     ("bonsai_p40_fwht_gemv_group", (NULL, NULL, NULL, 1, 16, NULL, 1024), 1),
     ("bonsai_p40_rmsnorm_fwht_quant", (16, 16, NULL, 16, 1000, 1, C.c_float(1e-6)), 1),   # n % 1024
