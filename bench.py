@@ -494,7 +494,7 @@ def valu_mfma_overlap(iters: int = 4096, per_cu: int = 4):
     blocks = per_cu * cus
     sink = torch.zeros(blocks, dtype=torch.int32, device="cuda")
     out = {}
-    for name, mode in (("mfma_only", 0), ("fma_only", 1), ("both", 2)):
+    for name, mode in (("mfma_only", 0), ("fma_only", 1), ("both", 2), ("gemm_core", 3)):
         B.overlap_probe(mode, 1, blocks, 64, sink)
         torch.cuda.synchronize()
         best = None
@@ -509,7 +509,23 @@ def valu_mfma_overlap(iters: int = 4096, per_cu: int = 4):
         out[name + "_us"] = round(best * 1e3, 2)
     out["both_over_sum"] = round(out["both_us"] / (out["mfma_only_us"] + out["fma_only_us"]), 3)
     out["both_over_max"] = round(out["both_us"] / max(out["mfma_only_us"], out["fma_only_us"]), 3)
+    # the GEMM's chunk step alone: iters steps per wave, 4 waves per SIMD, each
+    # step a 32 x 32 x 32 piece of the product; scaled to the M = 2048
+    # 17408x5120 prefill (5,570,560 such pieces over the CUs' SIMDs)
+    per_piece_ns = out["gemm_core_us"] * 1e3 / (iters * per_cu)
+    pieces = 2048 * N_FF * N_EMBD / 32768
+    out["gemm_core_ns_per_32x32x32_per_simd"] = round(per_piece_ns, 2)
+    out["gemm_core_floor_us_m2048_17408x5120"] = round(per_piece_ns * pieces / (4 * cus) / 1e3, 1)
     return out
+
+
+def launch_floor(steps: int = 200):
+    """us per launch of an empty kernel (256 workgroups of 64 threads) in a
+    HIP graph of back-to-back launches: what any launch that depends on the
+    one before it costs on this GPU, the floor under every decode kernel."""
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ms = time_loop(lambda i: B.launch_probe(256, 64, sink), steps, 10)
+    return ms * 1e3
 
 
 def kernel_source_hash():
@@ -578,6 +594,7 @@ def main():
         for kind in (0, 1):
             print(f"[bench] mfma peak kind {kind}: {mfma_peak(kind)}", flush=True)
         print(f"[bench] valu/mfma overlap: {valu_mfma_overlap()}", flush=True)
+        print(f"[bench] dependent launch floor: {launch_floor():.3f} us", flush=True)
         return
     if args.only_read:
         ms = bench_stream_read(gemv_bytes(N_FF, N_EMBD), args.steps, args.warmup)
@@ -655,6 +672,8 @@ def main():
         "4 independent v_mfma_f32_16x16x32_f16 and 16 independent fp32 FMAs per iteration per wave, "
         "4 waves per SIMD: both_over_sum near 1 means the VALU and the matrix core take turns"))
     print(f"[bench] valu/mfma overlap: {extra['valu_mfma_overlap']}", file=sys.stderr, flush=True)
+    extra["dependent_launch_floor_us"] = round(launch_floor(), 3)
+    print(f"[bench] dependent launch floor: {extra['dependent_launch_floor_us']} us", file=sys.stderr, flush=True)
     if not args.quick:
         for (n_out, n_in, tag) in ((N_EMBD, N_FF, "gemv_5120x17408"), (N_EMBD, N_EMBD, "gemv_5120x5120")):
             m = bench_gemv(n_out, n_in, args.steps, args.warmup, gen)

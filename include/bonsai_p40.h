@@ -355,8 +355,18 @@ int bonsai_p40_mfma_probe(int kind, int blocks, int iters, uint64_t * clk, uint3
 // v_mfma_f32_16x16x32_f16 (mode 0 or 2) and nf x 16 independent fp32 FMAs
 // (mode 1 or 2).  Time modes 0, 1 and 2 with events: mode 2 near the larger
 // of the other two means overlap, near their sum means the two pipes take
-// turns.  sink needs `blocks` words.  Errors: 1 on bad arguments.
+// turns.  Mode 3 is the prefill GEMM's chunk step alone (4 MFMAs with a zero
+// accumulator input, then 16 FMAs folding their results into accumulators;
+// nf unused): the floor of the GEMM's per-chunk cost without operand staging,
+// LDS reads and barriers.  sink needs `blocks` words.  Errors: 1 on bad
+// arguments.
 int bonsai_p40_overlap_probe(int mode, int nf, int blocks, int iters, uint32_t * sink, bonsai_stream stream);
+
+// Measurement: one empty kernel (`blocks` workgroups of `threads` threads,
+// 1..1024); replayed back to back it gives the cost of a launch that waits for
+// the one before it -- the floor under every kernel of a decode chain.
+// Errors: 1 on bad arguments.
+int bonsai_p40_launch_probe(int blocks, int threads, uint32_t * sink, bonsai_stream stream);
 
 #ifdef __cplusplus
 }

@@ -58,6 +58,7 @@ SIGNATURES = {
     "bonsai_p40_reload_tuning": [],
     "bonsai_p40_mfma_probe": [C.c_int, C.c_int, C.c_int, _V, _V, _V],
     "bonsai_p40_overlap_probe": [C.c_int, C.c_int, C.c_int, C.c_int, _V, _V],
+    "bonsai_p40_launch_probe": [C.c_int, C.c_int, _V, _V],
     "bonsai_p40_chain_plan_bytes": [C.c_int],
     "bonsai_p40_chain_plan": [_V, C.c_int, _V],
     "bonsai_p40_chain_run": [_V, C.c_int, _V, _V, _V],
@@ -310,6 +311,10 @@ def mfma_probe(kind: int, blocks: int, iters: int, clk, sink, stream=None) -> No
 def overlap_probe(mode: int, nf: int, blocks: int, iters: int, sink, stream=None) -> None:
     _check("bonsai_p40_overlap_probe",
            call("bonsai_p40_overlap_probe", mode, nf, blocks, iters, sink, stream=stream))
+
+
+def launch_probe(blocks: int, threads: int, sink, stream=None) -> None:
+    _check("bonsai_p40_launch_probe", call("bonsai_p40_launch_probe", blocks, threads, sink, stream=stream))
 
 
 def stream_read(buf, nbytes: int, out, blocks: int, stream=None) -> None:

@@ -140,16 +140,59 @@ overlap_probe_kernel(int iters, int nf, uint32_t * __restrict__ sink) {
     if (z == 1234.5f) sink[blockIdx.x] = 1u;       // practically never: keeps the work live
 }
 
+// The prefill GEMM's chunk step for one 32 x 32 wave tile, with nothing
+// else: 4 v_mfma_f32_16x16x32_f16 with a zero accumulator input, then the 16
+// fp32 FMAs that fold their results into the output accumulators with the
+// token scale -- compiler-scheduled, as in the GEMM.  The time per
+// iteration is the floor of the GEMM's per-chunk cost without operand
+// staging, LDS reads or barriers.
+__global__ void __launch_bounds__(256)
+gemm_core_probe_kernel(int iters, uint32_t * __restrict__ sink) {
+    const int lane = threadIdx.x & 63;
+    v8h a, b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        a[i] = (_Float16)(0.001f * (float)(lane + i));
+        b[i] = (_Float16)(0.002f * (float)(lane - i));
+    }
+    float acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.25f * (float)lane + (float)i;
+    const float da = 1.0001f + 1e-6f * (float)lane;
+    for (int it = 0; it < iters; ++it) {
+        v4f s[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[4 * t + i] = fmaf(da, s[t][i], acc[4 * t + i]);
+        a[0] += (_Float16)1.0f;                     // a new A operand every iteration
+    }
+    float z = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) z += acc[i];
+    if (z == 1234.5f) sink[blockIdx.x] = 1u;       // practically never: keeps the work live
+}
+
+// An empty kernel: the cost of a launch that depends on the one before it.
+__global__ void __launch_bounds__(1024) empty_probe_kernel(uint32_t * __restrict__ sink) {
+    if (threadIdx.x == 0x7fffffff) sink[0] = 1u;    // never
+}
+
 }  // namespace
 
 // VALU / MFMA overlap probe: `blocks` workgroups of 4 waves, each wave
-// iters x (4 MFMAs if mode != 1, nf x 16 FMAs if mode != 0).  sink needs
-// `blocks` words.  Errors: 1 on bad arguments.
+// iters x (4 MFMAs if mode != 1, nf x 16 FMAs if mode != 0); mode 3 is the
+// prefill GEMM's chunk step (4 MFMAs, then 16 FMAs on their results; nf
+// unused).  sink needs `blocks` words.  Errors: 1 on bad arguments.
 extern "C" int bonsai_p40_overlap_probe(int mode, int nf, int blocks, int iters, uint32_t * sink,
                                         bonsai_stream stream) {
-    if (blocks <= 0 || iters <= 0 || nf < 0 || nf > 16 || sink == nullptr || mode < 0 || mode > 2) return 1;
+    if (blocks <= 0 || iters <= 0 || nf < 0 || nf > 16 || sink == nullptr || mode < 0 || mode > 3) return 1;
     const hipStream_t st = (hipStream_t)stream;
-    if (mode == 0) hipLaunchKernelGGL(overlap_probe_kernel<0>, dim3((unsigned)blocks), dim3(256), 0, st, iters, nf, sink);
+    if (mode == 3) hipLaunchKernelGGL(gemm_core_probe_kernel, dim3((unsigned)blocks), dim3(256), 0, st, iters, sink);
+    else if (mode == 0) hipLaunchKernelGGL(overlap_probe_kernel<0>, dim3((unsigned)blocks), dim3(256), 0, st, iters, nf, sink);
     else if (mode == 1) hipLaunchKernelGGL(overlap_probe_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, st, iters, nf, sink);
     else hipLaunchKernelGGL(overlap_probe_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, st, iters, nf, sink);
     return (int)hipGetLastError();
@@ -169,6 +212,16 @@ extern "C" int bonsai_p40_mfma_probe(int kind, int blocks, int iters, uint64_t *
     else
         hipLaunchKernelGGL(mfma_probe_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, iters,
                            clk, sink);
+    return (int)hipGetLastError();
+}
+
+// Launch-cost probe: one empty kernel of `blocks` workgroups of `threads`
+// threads (1..1024).  Replayed back to back, its time per launch is what any
+// launch that depends on the one before it costs.  Errors: 1 on bad arguments.
+extern "C" int bonsai_p40_launch_probe(int blocks, int threads, uint32_t * sink, bonsai_stream stream) {
+    if (blocks <= 0 || threads <= 0 || threads > 1024 || sink == nullptr) return 1;
+    hipLaunchKernelGGL(empty_probe_kernel, dim3((unsigned)blocks), dim3((unsigned)threads), 0, (hipStream_t)stream,
+                       sink);
     return (int)hipGetLastError();
 }
 

@@ -69,6 +69,10 @@ NULL = None
     ("bonsai_p40_quant_gemv", (NULL, 16, NULL, 16, 1000), 1),          # n_in % 1024
     ("bonsai_p40_quant_gemv", (NULL, NULL, NULL, 16, 1024), 1),        # x NULL
     ("bonsai_p40_quant_gemv", (NULL, 16, NULL, 0, 1024), 0),           # empty no-op
+    ("bonsai_p40_launch_probe", (0, 64, 16), 1),
+    ("bonsai_p40_launch_probe", (1, 2048, 16), 1),
+    ("bonsai_p40_launch_probe", (1, 64, NULL), 1),
+    ("bonsai_p40_overlap_probe", (4, 1, 1, 1, 16), 1),                 # no mode 4
     ("bonsai_p40_gemv_group", (NULL, NULL, NULL, 1, NULL, 128), 1),   # NULL arrays
     ("bonsai_p40_fwht_gemv_group", (NULL, NULL, NULL, 1, 16, NULL, 1024), 1),
     ("bonsai_p40_rmsnorm_fwht_quant", (16, 16, NULL, 16, 1000, 1, C.c_float(1e-6)), 1),   # n % 1024
