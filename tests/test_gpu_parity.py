@@ -291,6 +291,46 @@ def test_fwht_gemv(n_out, n_in, signed):
     np.testing.assert_array_equal(bits(host(y)), bits(got))
 
 
+@pytest.mark.parametrize("n_out,n_in", [
+    (17408, 5120), (6144, 5120), (1024, 5120), (5120, 6144), (5120, 17408), (17407, 5120),
+    (333, 1024), (97, 10240), (100, 12288), (77, 2048), (64, 3072), (1, 5120)])
+def test_quant_gemv(n_out, n_in):
+    """y = W . Q8_1(x) in one launch: within the GEMV tolerance of the oracle,
+    x unchanged, and on the streaming widths bit-identical to
+    quant_activations + gemv (the reference hook's two launches)."""
+    case(f"quant_gemv {n_out}x{n_in}")
+    W = O.gen_weights(1650 + n_out + n_in, n_out, n_in)
+    x = O.gen_normal(1651 + n_in, n_in) * 1.5
+    Wd, xd = dev(W), dev(x)
+    y = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+    B.quant_gemv(Wd, xd, y, n_out, n_in)
+    got = host(y)
+    xq_ref = O.quantize_q8_1(x, True)
+    assert np.all(np.isfinite(got))
+    assert normwise(got, O.gemv(W, xq_ref, n_out, n_in, nthreads=16)) <= TOL
+    np.testing.assert_array_equal(bits(host(xd)), bits(x))
+    q = torch.zeros(n_in // 32 * 36, dtype=torch.uint8, device="cuda")
+    B.quant_activations(xd, q, n_in)
+    np.testing.assert_array_equal(host(q), xq_ref)
+    y2 = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+    B.gemv(Wd, q, y2, n_out, n_in)
+    if n_in // 128 in ROT_WIDTHS:
+        np.testing.assert_array_equal(bits(got), bits(host(y2)))
+
+
+@pytest.mark.parametrize("x_offset", [4, 8])
+def test_quant_gemv_unaligned_x(x_offset):
+    """x off a 16-byte boundary takes the generic kernel: same tolerance."""
+    case(f"quant_gemv unaligned x offset {x_offset}")
+    n_out, n_in = 300, 5120
+    W = O.gen_weights(1750, n_out, n_in)
+    x = O.gen_normal(1751, n_in)
+    buf, xp = offset_copy(x.view(np.uint8), x_offset)
+    y = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+    B.quant_gemv(dev(W), xp, y, n_out, n_in)
+    assert normwise(host(y), O.gemv(W, O.quantize_q8_1(x, True), n_out, n_in)) <= TOL
+
+
 GROUPS = [
     (5120, (6144, 1024, 1024)),               # q, k, v
     (5120, (17408, 17408)),                   # gate, up
