@@ -16,6 +16,11 @@
 //     allocated and nothing synchronises -- work is enqueued on `stream`;
 //   * return 1 for invalid arguments, 0 for an empty no-op, otherwise the
 //     hipError_t of the launch (so 0 = enqueued).  Callers test `!= 0`;
+//   * a NULL device pointer that the requested work would read or write is an
+//     invalid argument (1, nothing launched), where the reference launches
+//     anyway; optional pointers (signs, norm weights, status) may be NULL.
+//     The empty no-ops (n_out <= 0, n_tok <= 0, ...) still return 0 first, as
+//     in the reference;
 //   * block_pq2_0 = 34 bytes (fp16 d, 32 bytes of 2-bit codes, element j in
 //     byte j/4 at bits 2(j%4), value (code-1)*d); block_q8_1 = 36 bytes (fp16
 //     d, int16 sum s stored as raw bits, 32 int8 in the PQ2_0-native permuted

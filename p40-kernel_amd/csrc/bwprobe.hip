@@ -228,6 +228,7 @@ extern "C" int bonsai_p40_launch_probe(int blocks, int threads, uint32_t * sink,
 extern "C" int bonsai_p40_stream_read(const void * buf, int64_t bytes, uint32_t * out, int blocks,
                                       bonsai_stream stream) {
     if (bytes <= 0 || bytes % 16 != 0 || ((uintptr_t)buf & 15u) != 0 || blocks <= 0) return 1;
+    if (buf == nullptr || out == nullptr) return 1;
     hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
                        (const v4u *)buf, (size_t)bytes / 16, out);
     return (int)hipGetLastError();

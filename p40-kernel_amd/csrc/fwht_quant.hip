@@ -23,6 +23,7 @@
 #pragma clang fp contract(off)
 
 #include "fwht_device.h"
+#include "host_state.h"
 #include "../../include/bonsai_p40.h"
 
 using namespace pq2;
@@ -275,20 +276,20 @@ int bonsai_p40_fwht_signs_n(float * x, const float * signs, int64_t n, bonsai_st
 }
 
 int bonsai_p40_quant_activations(const float * x, void * out, int64_t n, bonsai_stream stream) {
-    if (n <= 0 || n % QK8 != 0 || !al4(out)) return 1;
+    if (n <= 0 || n % QK8 != 0 || !al4(out) || pq2host::any_null(x, out)) return 1;
     if (n / QK8 > 0x7fffffff - 128) return 1;
     return launch_quant(x, out, n, 1, false, (hipStream_t)stream);
 }
 
 int bonsai_p40_fwht_quant(const float * x, const float * signs, void * xq, int64_t n,
                           bonsai_stream stream) {
-    if (n <= 0 || n % HBLK != 0 || !al4(xq)) return 1;
+    if (n <= 0 || n % HBLK != 0 || !al4(xq) || pq2host::any_null(x, xq)) return 1;
     return launch_rot<M_ROT | M_OUT_Q8>(x, signs, nullptr, xq, n, 1, (hipStream_t)stream);
 }
 
 int bonsai_p40_quant_tokens(const float * X, const float * signs, void * Xq, int64_t n,
                             int64_t n_tok, int rotate, bonsai_stream stream) {
-    if (n <= 0 || n_tok <= 0 || n_tok > MAX_GRID_Y || !al4(Xq)) return 1;
+    if (n <= 0 || n_tok <= 0 || n_tok > MAX_GRID_Y || !al4(Xq) || pq2host::any_null(X, Xq)) return 1;
     if (n % (rotate ? HBLK : QK8) != 0) return 1;
     if (n * n_tok > ((int64_t)1 << 40)) return 1;
     if (rotate)
@@ -300,7 +301,7 @@ int bonsai_p40_quant_tokens(const float * X, const float * signs, void * Xq, int
 
 int bonsai_p40_rmsnorm_fwht_quant(const float * x, const float * w, const float * signs, void * xq,
                                   int64_t n, int64_t n_tok, float eps, bonsai_stream stream) {
-    if (n <= 0 || n % HBLK != 0 || x == nullptr || w == nullptr || !al4(xq)) return 1;
+    if (n <= 0 || n % HBLK != 0 || pq2host::any_null(x, w, xq) || !al4(xq)) return 1;
     if (n_tok <= 0) return 0;
     if (n_tok > 0x7fffffff || n > 0x7fffffff) return 1;
     const int nw = (int)(n / HBLK < 16 ? n / HBLK : 16);
@@ -326,7 +327,7 @@ int bonsai_p40_rmsnorm_fwht_quant(const float * x, const float * w, const float 
 
 int bonsai_p40_swiglu_fwht_quant(const float * gate, const float * up, const float * signs,
                                  void * xq, int64_t n, bonsai_stream stream) {
-    if (n <= 0 || n % HBLK != 0 || !al4(xq)) return 1;
+    if (n <= 0 || n % HBLK != 0 || !al4(xq) || pq2host::any_null(gate, up, xq)) return 1;
     if (n / HBLK > 0x7fffffff) return 1;
     const bool vec = al16(gate) && al16(up) && al16(signs);
     const dim3 grid((unsigned)(n / HBLK));

@@ -1208,7 +1208,7 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
                     int64_t n_tok, bonsai_stream stream) {
     if (n_in <= 0 || n_in % QK_PQ2 != 0) return 1;
     if (n_out <= 0 || n_tok <= 0) return 0;
-    if (((uintptr_t)Xq & 3u) != 0 || ((uintptr_t)W & 1u) != 0) return 1;
+    if (((uintptr_t)Xq & 3u) != 0 || ((uintptr_t)W & 1u) != 0 || pq2host::any_null(W, Xq, Y)) return 1;
     if (n_out > 0x7fffffff || n_tok > 0x7fffffff || n_in / QK_PQ2 > (1 << 24)) return 1;
     const int nb = (int)(n_in / QK_PQ2);
     hipStream_t st = (hipStream_t)stream;

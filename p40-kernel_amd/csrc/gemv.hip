@@ -1444,6 +1444,7 @@ int make_group(MatGroup & mg, const void * const * W, float * const * y, const i
         mg.W[m] = m < n_mat ? static_cast<const uint8_t *>(W[m]) : nullptr;
         mg.y[m] = m < n_mat ? y[m] : nullptr;
         mg.n_out[m] = r > 0 ? (int)r : 0;
+        if (r > 0 && pq2host::any_null(mg.W[m], mg.y[m])) return 1;
         *n_rows += mg.n_out[m];
     }
     return 0;
@@ -1631,7 +1632,7 @@ int bonsai_p40_gemv(const void * W, const void * xq, float * y, int64_t n_out, i
                     bonsai_stream stream) {
     if (n_in <= 0 || n_in % QK_PQ2 != 0 || ((uintptr_t)xq & 3u) != 0) return 1;
     if (n_out <= 0) return 0;
-    if (n_out > 0x3fffffff || n_in / QK_PQ2 > (1 << 24)) return 1;
+    if (n_out > 0x3fffffff || n_in / QK_PQ2 > (1 << 24) || pq2host::any_null(W, xq, y)) return 1;
     return gemv_group_dispatch<false>(single_group(W, y, n_out), 1, xq, nullptr, n_in, (hipStream_t)stream);
 }
 
@@ -1643,6 +1644,7 @@ int bonsai_p40_gemv_group(const void * const * W, float * const * y, const int64
     int64_t rows = 0;
     if (make_group(mg, W, y, n_out, n_mat, &rows) != 0) return 1;
     if (rows == 0) return 0;
+    if (xq == nullptr) return 1;
     return gemv_group_dispatch<false>(mg, n_mat, xq, nullptr, n_in, (hipStream_t)stream);
 }
 
@@ -1650,7 +1652,7 @@ int bonsai_p40_fwht_gemv(const void * W, const float * x, const float * signs, f
                          int64_t n_out, int64_t n_in, bonsai_stream stream) {
     if (n_in <= 0 || n_in % HBLK != 0 || x == nullptr) return 1;
     if (n_out <= 0) return 0;
-    if (n_out > 0x3fffffff || n_in / QK_PQ2 > (1 << 24)) return 1;
+    if (n_out > 0x3fffffff || n_in / QK_PQ2 > (1 << 24) || pq2host::any_null(W, y)) return 1;
     return fwht_gemv_group_dispatch(single_group(W, y, n_out), 1, x, signs, n_in, (hipStream_t)stream);
 }
 
@@ -1658,7 +1660,7 @@ int bonsai_p40_quant_gemv(const void * W, const float * x, float * y, int64_t n_
                           bonsai_stream stream) {
     if (n_in <= 0 || n_in % HBLK != 0 || x == nullptr) return 1;
     if (n_out <= 0) return 0;
-    if (n_out > 0x3fffffff || n_in / QK_PQ2 > (1 << 24)) return 1;
+    if (n_out > 0x3fffffff || n_in / QK_PQ2 > (1 << 24) || pq2host::any_null(W, y)) return 1;
     return quant_gemv_dispatch(single_group(W, y, n_out), x, n_in, (hipStream_t)stream);
 }
 
@@ -1722,7 +1724,7 @@ int bonsai_p40_chunk_dots(const void * W, const void * xq, int32_t * out, int64_
                           int64_t n_in, bonsai_stream stream) {
     if (n_in <= 0 || n_in % QK_PQ2 != 0 || ((uintptr_t)xq & 3u) != 0) return 1;
     if (n_out <= 0) return 0;
-    if (n_out > 0x3fffffff || n_in / QK_PQ2 > (1 << 24)) return 1;
+    if (n_out > 0x3fffffff || n_in / QK_PQ2 > (1 << 24) || pq2host::any_null(W, xq, out)) return 1;
     return gemv_group_dispatch<true>(single_group(W, nullptr, n_out), 1, xq, out, n_in, (hipStream_t)stream);
 }
 

@@ -11,6 +11,7 @@
 //    each filled exactly once (std::call_once).
 //  * Per-kernel attributes (the dynamic-LDS limit) are set once per kernel and
 //    device, also under std::call_once.
+// It also holds the NULL-pointer check every entry point applies.
 // Everything here is host code; inline functions with static locals have one
 // instance per process across the library's translation units.
 #pragma once
@@ -159,6 +160,13 @@ inline void once_per_device(PerDeviceOnce & o, Fn && fn) {
 inline void set_max_dynamic_lds(const void * kern, int bytes) {
     if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
         (void)hipGetLastError();
+}
+
+// Argument check shared by the entry points: true if any of the device
+// pointers the requested work reads or writes is NULL.
+template <class... P>
+inline bool any_null(const P *... p) {
+    return ((p == nullptr) || ...);
 }
 
 }  // namespace pq2host

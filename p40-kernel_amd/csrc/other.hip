@@ -38,7 +38,7 @@ int bonsai_p40_rmsnorm(const float * x, const float * w, float * y, int64_t n_ro
                        float eps, bonsai_stream stream) {
     if (n <= 0 || n > 0x7fffffff) return 1;
     if (n_rows <= 0) return 0;
-    if (n_rows > 0x7fffffff) return 1;
+    if (n_rows > 0x7fffffff || pq2host::any_null(x, w, y)) return 1;
     hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)n_rows), dim3(256), 0, (hipStream_t)stream,
                        x, w, y, (int)n, eps);
     return (int)hipGetLastError();

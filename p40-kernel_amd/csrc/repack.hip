@@ -147,7 +147,7 @@ int bonsai_p40_repack(const void * src, void * dst, int64_t n_out, int64_t n_in,
     if (n_in % QK_PQ2 != 0 || n_out <= 0 || n_in <= 0) return 1;
     const int64_t nb = n_in / QK_PQ2;
     if (nb % 8 != 0 || nb > (1 << 24)) return 1;
-    if ((((uintptr_t)src | (uintptr_t)dst) & 1u) != 0) return 1;
+    if ((((uintptr_t)src | (uintptr_t)dst) & 1u) != 0 || pq2host::any_null(src, dst)) return 1;
     const int64_t total = n_out * 4 * nb;
     int64_t blocks = (total + 255) / 256;
     if (blocks > 65535 * 8) blocks = 65535 * 8;
@@ -167,6 +167,7 @@ int bonsai_p40_gemv_repack(const void * W, const float * x, float * y, int64_t n
     const int64_t nb = n_in / QK_PQ2;
     if (nb % 8 != 0 || n_out > 0x7fffffff) return 1;
     if (((uintptr_t)W & 7u) != 0) return 1;            // 8-byte units must be aligned
+    if (pq2host::any_null(W, x, y)) return 1;
     const int rc = pq2::gemv_repack_streaming(W, x, y, n_out, n_in, stream);
     if (rc >= 0) return rc;
     const size_t lds = (size_t)nb * 4 * 40;

@@ -122,6 +122,62 @@ def _gpu_visible():
         return False
 
 
+A = 4096          # a 16-byte aligned placeholder address (never dereferenced: the check returns first)
+EPS = C.c_float(1e-6)
+
+# (entry, valid arguments, positions of the pointers that the work needs)
+NULL_CASES = [
+    ("bonsai_p40_gemv", (A, A, A, 16, 128), (0, 1, 2)),
+    ("bonsai_p40_chunk_dots", (A, A, A, 16, 128), (0, 1, 2)),
+    ("bonsai_p40_quant_activations", (A, A, 64), (0, 1)),
+    ("bonsai_p40_fwht_quant", (A, NULL, A, 1024), (0, 2)),
+    ("bonsai_p40_quant_tokens", (A, NULL, A, 1024, 2, 1), (0, 2)),
+    ("bonsai_p40_rmsnorm_fwht_quant", (A, A, NULL, A, 1024, 1, EPS), (0, 1, 3)),
+    ("bonsai_p40_swiglu_fwht_quant", (A, A, NULL, A, 1024), (0, 1, 3)),
+    ("bonsai_p40_gemm", (A, A, A, 16, 128, 4), (0, 1, 2)),
+    ("bonsai_p40_repack", (A, A, 4, 1024), (0, 1)),
+    ("bonsai_p40_gemv_repack", (A, A, A, 4, 1024), (0, 1, 2)),
+    ("bonsai_p40_fwht", (A, NULL, 1024), (0,)),
+    ("bonsai_p40_fwht_gemv", (A, A, NULL, A, 16, 1024), (0, 1, 3)),
+    ("bonsai_p40_quant_gemv", (A, A, A, 16, 1024), (0, 1, 2)),
+    ("bonsai_p40_rmsnorm", (A, A, A, 4, 64, EPS), (0, 1, 2)),
+    ("bonsai_p40_quantize_pq2_0", (A, A, 128), (0, 1)),
+    ("bonsai_p40_dequantize_pq2_0", (A, A, 128), (0, 1)),
+    ("bonsai_p40_stream_read", (A, 1024, A, 1), (0, 2)),
+]
+
+
+@pytest.mark.skipif(_gpu_visible(), reason="passes placeholder pointers: only where no GPU can run them")
+@pytest.mark.parametrize("name,args,ptrs", NULL_CASES, ids=[c[0] for c in NULL_CASES])
+def test_null_device_pointers_are_invalid(name, args, ptrs):
+    """A NULL pointer that the work would read or write returns 1 before any
+    launch (the reference would launch with it); the empty no-ops keep
+    returning 0 before that check."""
+    fn = getattr(B.lib(), name)
+    for k in ptrs:
+        bad = list(args)
+        bad[k] = NULL
+        assert fn(*bad, None) == 1, (name, k)
+
+
+@pytest.mark.skipif(_gpu_visible(), reason="passes placeholder pointers: only where no GPU can run them")
+def test_null_pointers_in_groups_are_invalid():
+    L = B.lib()
+    for fn, extra in ((L.bonsai_p40_gemv_group, (A, 128)),
+                      (L.bonsai_p40_fwht_gemv_group, (A, NULL, 1024)),
+                      (L.bonsai_p40_rmsnorm_fwht_gemv_group, (A, A, NULL, 1024, EPS))):
+        for hole in ("W", "y"):
+            W = (C.c_void_p * 2)(A, A)
+            y = (C.c_void_p * 2)(A, A)
+            (W if hole == "W" else y)[1] = None
+            n = (C.c_int64 * 2)(16, 16)
+            assert fn(W, y, n, 2, *extra, None) == 1, (fn, hole)
+        W = (C.c_void_p * 1)(A)
+        y = (C.c_void_p * 1)(A)
+        n = (C.c_int64 * 1)(16)
+        assert fn(W, y, n, 1, *((NULL,) + extra[1:]), None) == 1
+
+
 @pytest.mark.skipif(_gpu_visible(), reason="passes placeholder pointers: only where no GPU can run them")
 def test_concurrent_calls_from_host_threads():
     """Eight host threads call the launch paths (per-device property caches,
