@@ -5,8 +5,8 @@
 //
 // A ggml_tensor is passed as the handful of its fields the hook reads
 // (bonsai_ggml_tensor below: type, ne[4], nb[4], data, as in ggml.h), so the
-// library needs no ggml headers; the fork fills the view in a few lines
-// (INTEGRATION.md, section 4).  C++ header (it includes bonsai_p40.h).
+// library needs no ggml headers; the fork fills the view by copying those
+// fields from its ggml_tensor.  C++ header (it includes bonsai_p40.h).
 #pragma once
 
 #include "bonsai_p40.h"
