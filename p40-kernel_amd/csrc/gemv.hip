@@ -1188,6 +1188,20 @@ int launch_nb_small(const uint8_t * W, const uint8_t * X, float * Y, int n_out, 
     } else {
         MatGroup mg = single_group(W, Y, n_out);
         int per_cu = knob(pq2host::K_GEMV_WG_PER_CU, 0);
+        // 2 tokens on 5120-column rows: one 8-wave workgroup per CU once the
+        // units fill its waves, ring depth 1 up to 2 units per wave and 2
+        // beyond (MI355X, us, three 4-wave workgroups per CU -> this shape):
+        // 17408x5120 9.23 -> 9.02, 34816x5120 13.06 -> 12.89, 6144x5120 6.32
+        // -> 5.63, 4096x5120 5.41 -> 5.00; 2048x5120 keeps the 4-wave shape
+        // (4.29 against 4.97)
+        if constexpr (NT == 2 && NB == 40) {
+            const int64_t units = ((int64_t)n_out + NbSpec<NB, NT>::G - 1) / NbSpec<NB, NT>::G;
+            const int64_t waves8 = 8 * (int64_t)cu_count();
+            if (per_cu <= 0 && units > 2 * waves8)
+                return launch_nb_t<NB, 2, 8, false, 0, NT>(mg, 1, X, nullptr, nullptr, 1, st, n_tok);
+            if (per_cu <= 0 && units >= waves8)
+                return launch_nb_t<NB, 1, 8, false, 0, NT>(mg, 1, X, nullptr, nullptr, 1, st, n_tok);
+        }
         if (per_cu <= 0) per_cu = default_wg_per_cu(NB, (int64_t)n_out * PQ2_BYTES * NB);
         return launch_nb_t<NB, 2, 4, false, 0, NT>(mg, 1, X, nullptr, nullptr, per_cu, st, n_tok);
     }
