@@ -1188,13 +1188,14 @@ int launch_nb_small(const uint8_t * W, const uint8_t * X, float * Y, int n_out, 
     } else {
         MatGroup mg = single_group(W, Y, n_out);
         int per_cu = knob(pq2host::K_GEMV_WG_PER_CU, 0);
-        // 2 tokens on 5120-column rows: one 8-wave workgroup per CU once the
-        // units fill its waves, ring depth 1 up to 2 units per wave and 2
-        // beyond (MI355X, us, three 4-wave workgroups per CU -> this shape):
-        // 17408x5120 9.23 -> 9.02, 34816x5120 13.06 -> 12.89, 6144x5120 6.32
-        // -> 5.63, 4096x5120 5.41 -> 5.00; 2048x5120 keeps the 4-wave shape
-        // (4.29 against 4.97)
-        if constexpr (NT == 2 && NB == 40) {
+        // 2 tokens on 5120- and 6144-column rows: one 8-wave workgroup per CU
+        // once the units fill its waves, ring depth 1 up to 2 units per wave
+        // and 2 beyond (MI355X, us, three or two 4-wave workgroups per CU ->
+        // this shape): 17408x5120 9.23 -> 9.02, 34816x5120 13.06 -> 12.89,
+        // 6144x5120 6.32 -> 5.63, 4096x5120 5.41 -> 5.00, 5120x6144 5.40 ->
+        // 4.73, 6144x6144 5.47 -> 5.14, 2048x6144 4.27 -> 3.73; 2048x5120 (fewer
+        // units than waves) keeps the 4-wave shape (4.29 against 4.97)
+        if constexpr (NT == 2 && (NB == 40 || NB == 48)) {
             const int64_t units = ((int64_t)n_out + NbSpec<NB, NT>::G - 1) / NbSpec<NB, NT>::G;
             const int64_t waves8 = 8 * (int64_t)cu_count();
             if (per_cu <= 0 && units > 2 * waves8)

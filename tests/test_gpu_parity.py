@@ -557,6 +557,7 @@ def test_gemm_prefill_shapes_row_sample(n_out, n_in, n_tok):
 @pytest.mark.parametrize("n_out,n_in,n_tok", [
     (17408, 5120, 2), (6144, 5120, 3), (1025, 5120, 4), (5120, 6144, 2), (77, 6144, 4),
     (6144, 5120, 2), (4096, 5120, 2), (4095, 5120, 2), (2048, 5120, 2), (34816, 5120, 2),
+    (2048, 6144, 2), (6144, 6144, 2), (1024, 6144, 2),
     (333, 1024, 3), (64, 10240, 2), (31, 12288, 2), (17407, 5120, 2), (5120, 17408, 2),
     (301, 17408, 3), (100, 17408, 4), (257, 12288, 4), (5120, 17408, 4)])
 def test_gemm_small_batch_streaming(n_out, n_in, n_tok, knobs):
