@@ -839,12 +839,18 @@ int launch_bd_nt(const uint8_t * W, const uint8_t * X, float * Y, int n_out, int
 //              B4    6.76      7.49         7.95  8.67  7.72
 //              B5    8.70      7.86         8.25  9.31  8.18
 //              B8    8.94      8.48         8.62  9.20  8.37
-// (1 = 16 rows / K in 8, 2 = 16 / 4, 3 = 32 / 4, 4 = 32 / 8)
-int bd_choice(int nb, int64_t n_out, int64_t n_tok) {
+// (1 = 16 rows / K in 8, 2 = 16 / 4, 3 = 32 / 4, 4 = 32 / 8, 5 = 16 / 2).
+// 16 rows with K in 2 (about 19 KB of LDS: 8 workgroups per CU) wins where
+// all its workgroups are resident at once, at 6..8 tokens (us, 32/4 or 16/4
+// -> 16/2): 17408x5120 B8 14.12 -> 13.10, B6 13.55 -> 12.33, B5 12.34 ->
+// 12.29; with 34816 rows (a second round) 20.92 -> 23.67; at 6144x5120 B8
+// (7.28 -> 10.69) and 5120x17408 B8 (15.43 -> 30.60) the shapes above stay.
+int bd_choice(int nb, int64_t n_out, int64_t n_tok, int cus) {
     if (n_tok < 3 || n_tok > 8) return 0;
     const bool mfma4_width = nb == 8 || nb == 40 || nb == 48;
     if (mfma4_width && (n_tok == 4 || (n_tok == 3 && nb != 40))) return 0;
     if (nb >= 96) return n_tok >= 5 ? 4 : 1;
+    if (n_out >= 12288 && n_tok >= 6 && (n_out + 15) / 16 <= 8 * (int64_t)cus) return 5;
     if (n_out >= 12288 && n_tok >= 5) return n_tok >= 7 ? 3 : 2;
     return 1;
 }
@@ -1215,7 +1221,7 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
     const uint8_t * w = (const uint8_t *)W;
     const uint8_t * x = (const uint8_t *)Xq;
     if (n_tok == 1) return bonsai_p40_gemv(W, Xq, Y, n_out, n_in, stream);   // chunk-major == token-major
-    const int bd_cfg = knob(pq2host::K_GEMM_BD, -1) < 0 ? bd_choice(nb, n_out, n_tok)
+    const int bd_cfg = knob(pq2host::K_GEMM_BD, -1) < 0 ? bd_choice(nb, n_out, n_tok, gemm_cu_count())
                                                               : knob(pq2host::K_GEMM_BD, 0);
     if (bd_cfg > 0 && n_tok >= 3 && n_tok <= 8 && nb % 2 == 0 && nb >= 16 && ((uintptr_t)W & 3u) == 0 &&
         ((uintptr_t)Xq & 15u) == 0) {
@@ -1223,6 +1229,7 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
             case 2: return launch_bd_nt<1, 4>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
             case 3: return launch_bd_nt<2, 4>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
             case 4: return launch_bd_nt<2, 8>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
+            case 5: return launch_bd_nt<1, 2>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
             default: return launch_bd_nt<1, 8>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
         }
     }

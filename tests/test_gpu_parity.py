@@ -612,14 +612,14 @@ def test_gemm_small_batch_mfma4(n_out, n_in, n_tok, knobs):
         assert normwise(got[:, t], host(y)) <= 2 * TOL
 
 
-@pytest.mark.parametrize("cfg", ["auto", "1", "2", "3", "4"])
+@pytest.mark.parametrize("cfg", ["auto", "1", "2", "3", "4", "5"])
 @pytest.mark.parametrize("n_out,n_in,n_tok", [
     (17408, 5120, 8), (5120, 17408, 4), (6144, 5120, 5), (1000, 6144, 6), (77, 2048, 7),
     (33, 17408, 3), (5121, 12288, 8), (17, 10240, 4), (17408, 5120, 3), (5120, 6144, 8),
-    (5120, 17408, 8)])
+    (5120, 17408, 8), (17407, 5120, 6), (12289, 5120, 7)])
 def test_gemm_small_batch_block_diagonal(n_out, n_in, n_tok, cfg, knobs):
     """3..8 tokens on the block-diagonal 16x16x64 MFMA kernel in each of its
-    workgroup shapes (16 or 32 rows, K split 4 or 8 ways) and through the
+    workgroup shapes (16 or 32 rows, K split 2, 4 or 8 ways) and through the
     default choice: against the oracle and against one GEMV per token."""
     if cfg == "auto":
         knobs.unset("BONSAI_GEMM_BD")
