@@ -498,7 +498,7 @@ gemm_small_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X
     for (int k = 0; k < C::NIW; ++k) {
         const int idx = min(64 * k + lane, C::W_DW - 1);   // lanes past the piece re-read its last dword
         const int r = idx / 17, d = idx - 17 * r;
-        woff[k] = (uint32_t)(min(row0 + r, n_out - 1) * rs + 4 * d);
+        woff[k] = (uint32_t)(min(row0 + r, n_out - 1) * rs + 4 * d);   // W < 4 GiB (host)
     }
     // the 8 chunks of a piece are 8 * n_tok contiguous Q8_1 blocks of the
     // chunk-major X (288 * n_tok bytes, 16-byte aligned): dwordx4 DMA
@@ -682,7 +682,7 @@ gemm_bd_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
     for (int k = 0; k < C::NIW; ++k) {
         const int idx = min(64 * k + lane, C::W_DW - 1);   // lanes past the piece re-read its last dword
         const int r = idx / 17, d = idx - 17 * r;
-        woff[k] = (uint32_t)(min(row0 + r, n_out - 1) * rs + 4 * d);
+        woff[k] = (uint32_t)(min(row0 + r, n_out - 1) * rs + 4 * d);   // W < 4 GiB (host)
     }
     uint32_t aoff[C::NIA];
 #pragma unroll
@@ -1221,9 +1221,13 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
     const uint8_t * w = (const uint8_t *)W;
     const uint8_t * x = (const uint8_t *)Xq;
     if (n_tok == 1) return bonsai_p40_gemv(W, Xq, Y, n_out, n_in, stream);   // chunk-major == token-major
+    // the block-diagonal and streamed small-batch kernels address W with
+    // 32-bit per-lane offsets: a matrix of 4 GiB or more takes the kernels
+    // below them, which use 64-bit offsets
+    const bool off32 = (uint64_t)n_out * PQ2_BYTES * (uint64_t)nb < (1ull << 32);
     const int bd_cfg = knob(pq2host::K_GEMM_BD, -1) < 0 ? bd_choice(nb, n_out, n_tok, gemm_cu_count())
                                                               : knob(pq2host::K_GEMM_BD, 0);
-    if (bd_cfg > 0 && n_tok >= 3 && n_tok <= 8 && nb % 2 == 0 && nb >= 16 && ((uintptr_t)W & 3u) == 0 &&
+    if (off32 && bd_cfg > 0 && n_tok >= 3 && n_tok <= 8 && nb % 2 == 0 && nb >= 16 && ((uintptr_t)W & 3u) == 0 &&
         ((uintptr_t)Xq & 15u) == 0) {
         switch (bd_cfg) {
             case 2: return launch_bd_nt<1, 4>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
@@ -1239,7 +1243,7 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
     }
     const size_t skinny_lds = (size_t)4 * 16 * PQ2_BYTES * (nb / 4) + 4096;
     const int small_sel = knob(pq2host::K_GEMM_SMALL, 0);   // 0 streamed, 1 previous kernel
-    if (n_tok <= 16 && small_sel == 0 && nb % 2 == 0 && nb >= 8 && ((uintptr_t)W & 3u) == 0 &&
+    if (off32 && n_tok <= 16 && small_sel == 0 && nb % 2 == 0 && nb >= 8 && ((uintptr_t)W & 3u) == 0 &&
         ((uintptr_t)Xq & 15u) == 0) {
         switch (knob(pq2host::K_GEMM_SMALL_CFG, 0)) {
             case 1: return launch_small_nt<1, 4>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
