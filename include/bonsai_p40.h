@@ -62,14 +62,15 @@ int bonsai_p40_quant_activations(const float * x, void * out, int64_t n, bonsai_
 // Replaces include/bonsai_p40.h:29-30 (src/kernels/gemm_p40.cu:143-154).
 // n_tok == 1 runs the decode GEMV; 2 tokens the streaming kernel with
 // per-token activation planes; 3..8 the block-diagonal 16x16x64 int8 MFMA
-// kernel or, for 3..4 tokens on 1024-, 5120- and 6144-column rows, the 4x4x4
-// int8 MFMA streaming kernel; 9..16 the streamed 16x16x32 int8 MFMA kernel;
-// larger n_tok the f16-MFMA tile GEMM.  The GEMV and small-batch kernels
-// subtract each Q8_1 block's stored sum s as the reference does
-// (src/pq2_0.h:169); the f16 tile GEMM multiplies (code - 1) by q directly and
-// does not read s, so the two agree for blocks whose s is the sum of their q,
-// which holds for every block this library's or the reference's quantiser
-// writes.  Errors: 1 if n_in <= 0 or n_in % 128 != 0, Xq is not 4-byte or W
+// kernel, except 4 tokens on 1024-, 5120- and 6144-column rows and 3 on
+// 1024- and 6144-column rows, which take the 4x4x4 int8 MFMA streaming
+// kernel; 9..16 the streamed 16x16x32 int8 MFMA kernel; larger n_tok the
+// f16-MFMA tile GEMM (other alignments: 64-bit-offset MFMA kernels).  The
+// GEMV and the streamed small-batch kernels subtract each Q8_1 block's
+// stored sum s as the reference does (src/pq2_0.h:169); the tile GEMMs and
+// the kernels for other alignments multiply (code - 1) by q directly and do
+// not read s.  The two agree for blocks whose s is the sum of their q, which
+// holds for every block this library's or the reference's quantiser writes.  Errors: 1 if n_in <= 0 or n_in % 128 != 0, Xq is not 4-byte or W
 // not 2-byte aligned, or n_out, n_tok or n_in / 128 is too large for the
 // launch; 0 (no-op) if n_out <= 0 or n_tok <= 0.
 int bonsai_p40_gemm(const void * W, const void * Xq, float * Y,
