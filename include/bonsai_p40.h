@@ -168,8 +168,9 @@ int bonsai_p40_swiglu_fwht_quant(const float * gate, const float * up, const flo
 // the model widths (n_in/128 in {8, 40, 48, 80, 96, 136}) with 16-byte
 // aligned W, x and signs, y is bit-identical to the two-call sequence.  x is
 // not modified; signs may be NULL.  Errors: 1 if n_in <= 0, n_in % 1024 != 0,
-// x is NULL, or (other widths) the Q8_1 activation does not fit in LDS
-// (n_in > 130048); 0 (no-op) if n_out <= 0.
+// x is NULL, or (other widths) the Q8_1 activation, 36 bytes per 32 columns,
+// does not fit in a workgroup's LDS less 1 KiB (n_in > 144384 with MI355X's
+// 160 KiB); 0 (no-op) if n_out <= 0.
 int bonsai_p40_fwht_gemv(const void * W, const float * x, const float * signs, float * y,
                          int64_t n_out, int64_t n_in, bonsai_stream stream);
 
@@ -181,7 +182,8 @@ int bonsai_p40_fwht_gemv(const void * W, const float * x, const float * signs, f
 // the quantiser's device code (host rounding); on the model widths with
 // 16-byte aligned W and x, y is bit-identical to the two-call sequence.
 // Errors: 1 if n_in <= 0, n_in % 1024 != 0, x is NULL, or (other widths) the
-// Q8_1 activation does not fit in LDS (n_in > 130048); 0 (no-op) if n_out <= 0.
+// Q8_1 activation does not fit in a workgroup's LDS less 1 KiB (n_in > 144384
+// with MI355X's 160 KiB); 0 (no-op) if n_out <= 0.
 int bonsai_p40_quant_gemv(const void * W, const float * x, float * y, int64_t n_out, int64_t n_in,
                           bonsai_stream stream);
 
