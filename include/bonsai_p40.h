@@ -135,8 +135,9 @@ int bonsai_p40_fwht_quant(const float * x, const float * signs, void * xq, int64
 // is optionally rotated (rotate != 0: FWHT with signs, n % 1024 == 0) and
 // quantised on its own, written chunk-major (block (c, t) at c*n_tok + t) --
 // the Xq layout bonsai_p40_gemm consumes, which the reference API has no
-// producer for.  Errors: 1 if n <= 0, n % 32 != 0 (n % 1024 with rotate) or
-// n_tok <= 0.
+// producer for.  Errors: 1 if n <= 0, n % 32 != 0 (n % 1024 with rotate),
+// n_tok <= 0 or n_tok > 65535 (one grid row per token), n * n_tok > 2^40, X or
+// Xq is NULL, Xq is not 4-byte aligned, or signs is given without rotate.
 int bonsai_p40_quant_tokens(const float * X, const float * signs, void * Xq, int64_t n,
                             int64_t n_tok, int rotate, bonsai_stream stream);
 

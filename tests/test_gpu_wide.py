@@ -8,7 +8,8 @@ the whole Q8_1 activation (36 bytes per 32 columns) in a workgroup's LDS less
 not, and that call must return 1 and launch nothing.  The quantisers, the
 int32 chunk dots, the GEMV, the fused and RMSNorm-fused GEMVs and the GEMM
 (2 ... 40 tokens) are checked at these widths: bytes and int32 dots exactly,
-fp32 outputs within 1e-5 of the oracle."""
+fp32 outputs within 1e-5 of the oracle.  The chunk-major token quantiser is
+checked at its token limit (65535, one grid row per token)."""
 import numpy as np
 import pytest
 
@@ -138,3 +139,21 @@ def test_wide_gemm(n_in, n_tok):
     assert np.all(np.isfinite(got))
     ref = O.gemm(W, Xq, N_OUT, n_in, n_tok, nthreads=16).reshape(N_OUT, n_tok)
     assert rel_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("rotate", [1, 0])
+def test_token_quantiser_at_its_token_limit(rotate):
+    """bonsai_p40_quant_tokens runs one grid row per token: 65535 tokens are
+    the most it takes (bytes exact), 65536 return 1 and write nothing."""
+    n, n_tok = 1024, 65535
+    case(f"chunk-major token quantiser, {n_tok} tokens of {n}, rotate={rotate}")
+    X = O.gen_normal(10_700 + rotate, n * n_tok).reshape(n_tok, n)
+    Xd = dev(X.astype(np.float32))
+    Xq = torch.empty(B.q8_bytes(n, n_tok), dtype=torch.uint8, device="cuda")
+    B.quant_tokens(Xd, None, Xq, n, n_tok, bool(rotate))
+    ref = O.quantize_chunk_major(O.fwht(X.ravel()).reshape(n_tok, n) if rotate else X)
+    assert np.array_equal(host(Xq), ref)
+    big = torch.zeros((n_tok + 1) * n, dtype=torch.float32, device="cuda")
+    out = torch.full((B.q8_bytes(n, n_tok + 1),), 0x5A, dtype=torch.uint8, device="cuda")
+    assert B.call("bonsai_p40_quant_tokens", big, None, out, n, n_tok + 1, rotate) == 1
+    assert bool((out == 0x5A).all()), "a rejected call wrote its output"
