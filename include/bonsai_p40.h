@@ -47,7 +47,7 @@ typedef void * bonsai_stream;
 // y[n_out] = W[n_out, n_in] . x with x already in permuted Q8_1 (xq).
 // Replaces include/bonsai_p40.h:21-22 (src/kernels/gemv_p40.cu:210-219).
 // Errors: 1 if n_in <= 0 or n_in % 128 != 0 or xq is not 4-byte aligned;
-// 0 (no-op) if n_out <= 0.
+// 0 (no-op) if n_out <= 0; then 1 if n_out >= 2^30 or n_in / 128 > 2^24.
 int bonsai_p40_gemv(const void * W, const void * xq, float * y,
                     int64_t n_out, int64_t n_in, bonsai_stream stream);
 
@@ -85,8 +85,10 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y,
 int bonsai_p40_repack(const void * src, void * dst, int64_t n_out, int64_t n_in, bonsai_stream stream);
 // y = W_repacked . x for fp32 x (quantised to Q8_1 inside the kernel).
 // Replaces include/bonsai_p40.h:36-37 (src/kernels/gemv_repack_p40.cu:209-220).
-// Errors: as bonsai_p40_repack, plus 1 if the quantised activation
-// (n_in/32 * 40 bytes) does not fit the 160 KiB LDS of a workgroup.
+// Errors: as bonsai_p40_repack, plus 1 if W is not 8-byte aligned (its 8-byte
+// code units are read whole) or, on widths without the streaming kernel, the
+// quantised activation (n_in/32 * 40 bytes) does not fit the 160 KiB LDS of a
+// workgroup.
 int bonsai_p40_gemv_repack(const void * W, const float * x, float * y,
                            int64_t n_out, int64_t n_in, bonsai_stream stream);
 

@@ -178,6 +178,26 @@ def test_null_pointers_in_groups_are_invalid():
         assert fn(W, y, n, 1, *((NULL,) + extra[1:]), None) == 1
 
 
+LIMIT_CASES = [
+    ("gemv: n_out >= 2^30", "bonsai_p40_gemv", (A, A, A, 1 << 30, 128)),
+    ("gemv: n_in / 128 > 2^24", "bonsai_p40_gemv", (A, A, A, 16, 128 * ((1 << 24) + 1))),
+    ("gemv_repack: W not 8-byte aligned", "bonsai_p40_gemv_repack", (A + 4, A, A, 4, 1024)),
+    ("gemm: W not 2-byte aligned", "bonsai_p40_gemm", (A + 1, A, A, 16, 128, 4)),
+    ("fwht_quant: xq not 4-byte aligned", "bonsai_p40_fwht_quant", (A, NULL, A + 2, 1024)),
+    ("quant_tokens: more than 65535 tokens", "bonsai_p40_quant_tokens", (A, NULL, A, 1024, 65536, 1)),
+    ("quant_tokens: n * n_tok > 2^40", "bonsai_p40_quant_tokens", (A, NULL, A, 1 << 30, 2048, 0)),
+    ("quant_tokens: signs without the rotation", "bonsai_p40_quant_tokens", (A, A, A, 1024, 2, 0)),
+]
+
+
+@pytest.mark.skipif(_gpu_visible(), reason="passes placeholder pointers: only where no GPU can run them")
+@pytest.mark.parametrize("what,name,args", LIMIT_CASES, ids=[c[0] for c in LIMIT_CASES])
+def test_documented_limits_are_invalid(what, name, args):
+    """The size and alignment limits the header states return 1 before any
+    launch."""
+    assert getattr(B.lib(), name)(*args, None) == 1, what
+
+
 @pytest.mark.skipif(_gpu_visible(), reason="passes placeholder pointers: only where no GPU can run them")
 def test_concurrent_calls_from_host_threads():
     """Eight host threads call the launch paths (per-device property caches,
