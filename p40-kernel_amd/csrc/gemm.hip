@@ -1158,16 +1158,25 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
 #pragma unroll
                     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[mi][ni][i]));
         };
+        // the conversion of the next block runs at raised wave priority: the
+        // barrier below waits for the last wave's conversion, so the arbiter
+        // serves it ahead of other waves' MFMA and epilogue work (MI355X, one
+        // process, min us, default -> raised: 17408x5120 M = 2048 545 -> 522,
+        // 5120x17408 M = 2048 549 -> 534, M = 512 198 -> 180; priorities 1, 2
+        // and 3 measured alike; raising the MFMA phase instead moved nothing)
         issue(0);
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
+            __builtin_amdgcn_s_setprio(0);
             if (p < 3) issue(p + 1);
             __builtin_amdgcn_sched_barrier(0);
             epilogue(p);
             __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(1);
             commit_part(next, st ^ 1, p);
             __builtin_amdgcn_sched_barrier(0);
         }
+        __builtin_amdgcn_s_setprio(0);
         __syncthreads();
     };
 
