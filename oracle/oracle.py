@@ -132,6 +132,10 @@ def quantize_chunk_major(x: np.ndarray) -> np.ndarray:
 
 def fwht(x: np.ndarray, signs: np.ndarray | None = None) -> np.ndarray:
     y = np.array(x, dtype=np.float32, copy=True)
+    if y.size % HBLK != 0:      # the C restatement walks whole 1024-blocks
+        raise ValueError(f"fwht: length {y.size} is not a multiple of {HBLK}")
+    if signs is not None and np.size(signs) < y.size:
+        raise ValueError("fwht: the sign vector is shorter than x")
     s = None if signs is None else np.ascontiguousarray(signs, dtype=np.float32)
     lib().orc_fwht_blocks(_p(y, _f32p), None if s is None else _p(s, _f32p), y.size)
     return y

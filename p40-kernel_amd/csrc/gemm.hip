@@ -1209,12 +1209,63 @@ gemm_f16_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
         }
 }
 
+// The 128-row f16 prefill kernel (gemm_f16_kernel) over rows [0, n_out) of w / Y.
+int gemm_prefill_f16(const uint8_t * w, const uint8_t * x, float * Y, int64_t n_out, int64_t n_tok, int nb,
+                     hipStream_t st) {
+    // 16 waves (4 per SIMD, 32 x 32 wave tiles) measured 12-22 % faster than
+    // 8 waves (2 per SIMD, 64 x 32) on every prefill shape: the latency of
+    // the chunk pipeline and the per-block barrier is hidden by more waves.
+    // One workgroup fits a CU: where even twice the 128-token tiles fit in
+    // one round, 64-token tiles put twice the CUs to work (6144x5120 at
+    // M = 256: 61 -> 42 us); past that the extra round costs more than the
+    // idle CUs (5120x17408 at M = 512: 200 -> 256 us), so 128.
+    const int64_t tiles128 = cdiv(n_out, GF_BM) * cdiv(n_tok, 128);
+    int bn = knob(pq2host::K_GEMM_F16_BN, 0);
+    if (bn != 64 && bn != 128) bn = 2 * tiles128 <= gemm_cu_count() ? 64 : 128;
+    // A last round that only part-fills the CUs (17408 rows at M = 512:
+    // 544 tiles = 2 rounds + 32 tiles) costs a whole round.  Where the
+    // full rounds cover whole row tiles, they run as one launch and the
+    // remaining rows as a second launch of 64-token tiles, which spreads
+    // them over more CUs (twice the tiles, each about half the work).
+    const int cus = gemm_cu_count();
+    const int64_t ttok = cdiv(n_tok, 128), rounds = tiles128 / cus, rest = tiles128 - rounds * cus;
+    if (bn == 128 && rounds >= 1 && rest > 0 && 2 * rest <= cus && (rounds * cus) % ttok == 0 &&
+        knob(pq2host::K_GEMM_F16_SPLIT, 1) > 0 && knob(pq2host::K_GEMM_F16_WAVES, 16) != 8) {
+        const int64_t rows_main = rounds * cus / ttok * GF_BM;
+        const int64_t rows_tail = n_out - rows_main;
+        if (rows_tail > 0 && cdiv(rows_tail, GF_BM) * cdiv(n_tok, 64) <= cus) {
+            hipLaunchKernelGGL((gemm_f16_kernel<4, 4, 2, 2>), dim3((unsigned)(rows_main / GF_BM), (unsigned)ttok),
+                               dim3(1024), 0, st, w, x, Y, (int)rows_main, (int)n_tok, nb);
+            hipLaunchKernelGGL((gemm_f16_kernel<4, 4, 2, 1, 64>),
+                               dim3((unsigned)cdiv(rows_tail, GF_BM), (unsigned)cdiv(n_tok, 64)), dim3(1024), 0,
+                               st, w + (size_t)rows_main * PQ2_BYTES * nb, x, Y + (size_t)rows_main * n_tok,
+                               (int)rows_tail, (int)n_tok, nb);
+            return (int)hipGetLastError();
+        }
+    }
+    const dim3 grid((unsigned)cdiv(n_out, GF_BM), (unsigned)cdiv(n_tok, bn));
+    if (knob(pq2host::K_GEMM_F16_WAVES, 16) == 8)
+        hipLaunchKernelGGL((gemm_f16_kernel<2, 4, 4, 2>), dim3(grid.x, (unsigned)cdiv(n_tok, 128)), dim3(512),
+                           0, st, w, x, Y, (int)n_out, (int)n_tok, nb);
+    else if (bn == 64)
+        hipLaunchKernelGGL((gemm_f16_kernel<4, 4, 2, 1, 64>), grid, dim3(1024), 0, st, w, x, Y, (int)n_out,
+                           (int)n_tok, nb);
+    else
+        hipLaunchKernelGGL((gemm_f16_kernel<4, 4, 2, 2>), grid, dim3(1024), 0, st, w, x, Y, (int)n_out, (int)n_tok, nb);
+    return (int)hipGetLastError();
+}
+
 }  // namespace
 
 namespace pq2 {
 // gemv.hip: 2..4 tokens on the streaming kernels; -1 if not applicable
 int gemv_small_batch(const void * W, const void * Xq, float * Y, int64_t n_out, int64_t n_in,
                      int64_t n_tok, bonsai_stream stream);
+// gemm_wide.hip: rows [0, rows) that the wide kernel takes (0: none) and its launch
+int64_t gemm_wide_rows(const void * W, const void * Xq, int64_t n_out, int64_t n_tok, int nb, int cus, bool force,
+                       int * mi);
+int gemm_wide_launch(const void * W, const void * Xq, float * Y, int64_t n_out, int64_t n_tok, int nb, int mi,
+                     hipStream_t st);
 }
 
 extern "C" {
@@ -1276,46 +1327,20 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
         return (int)hipGetLastError();
     }
     if (knob(pq2host::K_GEMM_KERNEL, 0) == 0) {
-        // 16 waves (4 per SIMD, 32 x 32 wave tiles) measured 12-22 % faster than
-        // 8 waves (2 per SIMD, 64 x 32) on every prefill shape: the latency of
-        // the chunk pipeline and the per-block barrier is hidden by more waves.
-        // One workgroup fits a CU: where even twice the 128-token tiles fit in
-        // one round, 64-token tiles put twice the CUs to work (6144x5120 at
-        // M = 256: 61 -> 42 us); past that the extra round costs more than the
-        // idle CUs (5120x17408 at M = 512: 200 -> 256 us), so 128.
-        const int64_t tiles128 = cdiv(n_out, GF_BM) * cdiv(n_tok, 128);
-        int bn = knob(pq2host::K_GEMM_F16_BN, 0);
-        if (bn != 64 && bn != 128) bn = 2 * tiles128 <= gemm_cu_count() ? 64 : 128;
-        // A last round that only part-fills the CUs (17408 rows at M = 512:
-        // 544 tiles = 2 rounds + 32 tiles) costs a whole round.  Where the
-        // full rounds cover whole row tiles, they run as one launch and the
-        // remaining rows as a second launch of 64-token tiles, which spreads
-        // them over more CUs (twice the tiles, each about half the work).
-        const int cus = gemm_cu_count();
-        const int64_t ttok = cdiv(n_tok, 128), rounds = tiles128 / cus, rest = tiles128 - rounds * cus;
-        if (bn == 128 && rounds >= 1 && rest > 0 && 2 * rest <= cus && (rounds * cus) % ttok == 0 &&
-            knob(pq2host::K_GEMM_F16_SPLIT, 1) > 0 && knob(pq2host::K_GEMM_F16_WAVES, 16) != 8) {
-            const int64_t rows_main = rounds * cus / ttok * GF_BM;
-            const int64_t rows_tail = n_out - rows_main;
-            if (rows_tail > 0 && cdiv(rows_tail, GF_BM) * cdiv(n_tok, 64) <= cus) {
-                hipLaunchKernelGGL((gemm_f16_kernel<4, 4, 2, 2>), dim3((unsigned)(rows_main / GF_BM), (unsigned)ttok),
-                                   dim3(1024), 0, st, w, x, Y, (int)rows_main, (int)n_tok, nb);
-                hipLaunchKernelGGL((gemm_f16_kernel<4, 4, 2, 1, 64>),
-                                   dim3((unsigned)cdiv(rows_tail, GF_BM), (unsigned)cdiv(n_tok, 64)), dim3(1024), 0,
-                                   st, w + (size_t)rows_main * PQ2_BYTES * nb, x, Y + (size_t)rows_main * n_tok,
-                                   (int)rows_tail, (int)n_tok, nb);
-                return (int)hipGetLastError();
+        // long prompts: the 256-row wide kernel (gemm_wide.hip) over the rows
+        // whose tiles fill whole rounds of CUs, the 128-row kernel for the rest
+        const int wide = knob(pq2host::K_GEMM_WIDE, 1);
+        if (wide != 0 && n_tok > 16) {
+            int mi = 8;
+            const int64_t rows = pq2::gemm_wide_rows(W, Xq, n_out, n_tok, nb, gemm_cu_count(), wide == 2, &mi);
+            if (rows > 0) {
+                const int rc = pq2::gemm_wide_launch(W, Xq, Y, rows, n_tok, nb, mi, st);
+                if (rc != 0 || rows == n_out) return rc;
+                return gemm_prefill_f16(w + (size_t)rows * PQ2_BYTES * nb, x, Y + (size_t)rows * n_tok,
+                                        n_out - rows, n_tok, nb, st);
             }
         }
-        const dim3 grid((unsigned)cdiv(n_out, GF_BM), (unsigned)cdiv(n_tok, bn));
-        if (knob(pq2host::K_GEMM_F16_WAVES, 16) == 8)
-            hipLaunchKernelGGL((gemm_f16_kernel<2, 4, 4, 2>), dim3(grid.x, (unsigned)cdiv(n_tok, 128)), dim3(512),
-                               0, st, w, x, Y, (int)n_out, (int)n_tok, nb);
-        else if (bn == 64)
-            hipLaunchKernelGGL((gemm_f16_kernel<4, 4, 2, 1, 64>), grid, dim3(1024), 0, st, w, x, Y, (int)n_out,
-                               (int)n_tok, nb);
-        else
-            hipLaunchKernelGGL((gemm_f16_kernel<4, 4, 2, 2>), grid, dim3(1024), 0, st, w, x, Y, (int)n_out, (int)n_tok, nb);
+        return gemm_prefill_f16(w, x, Y, n_out, n_tok, nb, st);
     } else if ((nb & 1) || ((uintptr_t)W & 3u) != 0) {
         dim3 grid((unsigned)cdiv(n_out, 64), (unsigned)cdiv(n_tok, 64));
         hipLaunchKernelGGL(gemm_mfma_kernel_u16, grid, dim3(256), 0, st, w, x, Y, (int)n_out, (int)n_tok, nb);

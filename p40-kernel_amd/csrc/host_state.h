@@ -43,6 +43,8 @@ enum Knob : int {
     K_GEMM_F16_BN,
     K_GEMM_F16_SPLIT,
     K_GEMM_F16_WAVES,
+    K_GEMM_WIDE,
+    K_GEMM_WIDE_MI,
     K_GGML_ENABLE,
     K_GGML_VERBOSE,
     K_COUNT
@@ -55,8 +57,8 @@ inline const char * knob_name(int k) {
         "BONSAI_MFMA4_MIN_TOK",       "BONSAI_FGEMV_WAVES",     "BONSAI_FGEMV_OVL",
         "BONSAI_GEMM_SMALL_GEMV",     "BONSAI_GEMM_BD",         "BONSAI_GEMM_SMALL",
         "BONSAI_GEMM_SMALL_CFG",      "BONSAI_GEMM_KERNEL",     "BONSAI_GEMM_F16_BN",
-        "BONSAI_GEMM_F16_SPLIT",      "BONSAI_GEMM_F16_WAVES",  "BONSAI_P40",
-        "BONSAI_P40_VERBOSE",
+        "BONSAI_GEMM_F16_SPLIT",      "BONSAI_GEMM_F16_WAVES",  "BONSAI_GEMM_WIDE",
+        "BONSAI_GEMM_WIDE_MI",        "BONSAI_P40",             "BONSAI_P40_VERBOSE",
     };
     return names[k];
 }

@@ -94,6 +94,28 @@ def test_graph_replays_of_gemv_gemm_and_fused_launches():
     replay_and_check(g, outs, refs, lambda: B.gemv(W, xq, other, n_out, n_in))
 
 
+@pytest.mark.parametrize("wide,n_out,n_tok", [("2", 600, 300), ("1", 17408, 1024)])
+def test_graph_replays_of_wide_prefill_gemm(wide, n_out, n_tok, knobs):
+    """The wide prefill kernel in a graph: forced on a ragged shape, and by
+    the default rule on a shape it splits into the wide launch and the
+    128-row launch for the remaining rows."""
+    knobs.set("BONSAI_GEMM_WIDE", wide)
+    case(f"graph: prefill GEMM {n_out}x5120x{n_tok}, BONSAI_GEMM_WIDE={wide}")
+    n_in = 5120
+    W = dev(O.gen_weights(9150, n_out, n_in))
+    Xq = dev(O.quantize_chunk_major(O.gen_normal(9151, n_tok * n_in).reshape(n_tok, n_in)))
+    Y = torch.empty(n_out * n_tok, dtype=torch.float32, device="cuda")
+
+    def launches():
+        B.gemm(W, Xq, Y, n_out, n_in, n_tok)
+
+    launches()
+    refs = [snap(Y)]
+    g = capture(launches)
+    other = torch.empty(n_out * n_tok, dtype=torch.float32, device="cuda")
+    replay_and_check(g, [Y], refs, lambda: B.gemm(W, Xq, other, n_out, n_in, n_tok), n=3)
+
+
 @pytest.mark.parametrize("noalloc", [False, True])
 def test_graph_replays_of_ffn_launch(noalloc):
     """Two FFN gate/up launches per graph: the second launch starts from the

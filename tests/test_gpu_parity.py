@@ -758,6 +758,67 @@ def test_gemm_split_last_round(n_out, n_in, n_tok, knobs):
     assert normwise(got["1"][rows], ref) <= TOL
 
 
+@pytest.mark.parametrize("mi", ["8", "5"])
+@pytest.mark.parametrize("n_out,n_in,n_tok", [(1000, 5120, 300), (300, 1024, 77), (257, 2048, 513),
+                                              (999, 6144, 1000), (40, 256, 17), (161, 17408, 260)])
+def test_gemm_wide_kernel(mi, n_out, n_in, n_tok, knobs):
+    """The wide prefill kernel (256- or 160-row tiles, 256 tokens) forced on
+    ragged shapes: partial row and token tiles, two blocks per row up to 136.
+    Bit-identical to the 128-row kernel (both add the chunks' products in K
+    order with the same FMA), and against the oracle."""
+    case(f"gemm wide kernel {n_out}x{n_in}x{n_tok} ({mi} x 32 rows)")
+    W = O.gen_weights(3400 + n_out, n_out, n_in)
+    X = np.stack([O.gen_normal(3401 + t, n_in) for t in range(n_tok)])
+    if n_in % 1024 == 0:
+        X = np.stack([O.fwht(x) for x in X])
+    Xq = O.quantize_chunk_major(X)
+    Wd, Xd = dev(W), dev(Xq)
+    got = {}
+    knobs.set("BONSAI_GEMM_WIDE_MI", mi)
+    for wide in ("2", "0"):
+        knobs.set("BONSAI_GEMM_WIDE", wide)
+        Y = torch.full((n_out, n_tok), float("nan"), dtype=torch.float32, device="cuda")
+        B.gemm(Wd, Xd, Y, n_out, n_in, n_tok)
+        got[wide] = host(Y)
+    assert np.all(np.isfinite(got["2"]))
+    np.testing.assert_array_equal(bits(got["2"]), bits(got["0"]))
+    assert normwise(got["2"], O.gemm(W, Xq, n_out, n_in, n_tok, nthreads=16)) <= TOL
+
+
+@pytest.mark.parametrize("mi", ["8", "5"])
+def test_gemm_wide_kernel_edge_scales(mi, knobs):
+    """The wide kernel on blocks with subnormal or zero scales and on blocks
+    with |d| >= 32768 holding code 3 (staged as d / 2, a second pass adds the
+    other half): against the oracle and bit-identical to the 128-row kernel."""
+    case(f"gemm wide kernel 300x2048x300 edge scales ({mi} x 32 rows)")
+    n_out, n_in, n_tok = 300, 2048, 300
+    W = O.gen_weights(3500, n_out, n_in).copy()
+    nb = n_in // 128
+    rng = np.random.default_rng(35)
+    for r in range(n_out):
+        for b in rng.choice(nb, 3, replace=False):
+            off = (r * nb + b) * 34
+            if r % 3 == 0:
+                bits16 = np.uint16(rng.integers(0x7800, 0x7C00) | (0x8000 if rng.random() < 0.5 else 0))
+                W[off + 2:off + 34] = rng.integers(0, 256, 32, dtype=np.uint8)
+            else:
+                bits16 = np.uint16(rng.integers(0, 1024))
+            W[off:off + 2] = np.frombuffer(bits16.tobytes(), np.uint8)
+    X = O.gen_normal(3501, n_tok * n_in).reshape(n_tok, n_in)
+    Xq = O.quantize_chunk_major(X)
+    Wd, Xd = dev(W), dev(Xq)
+    got = {}
+    knobs.set("BONSAI_GEMM_WIDE_MI", mi)
+    for wide in ("2", "0"):
+        knobs.set("BONSAI_GEMM_WIDE", wide)
+        Y = torch.full((n_out, n_tok), float("nan"), dtype=torch.float32, device="cuda")
+        B.gemm(Wd, Xd, Y, n_out, n_in, n_tok)
+        got[wide] = host(Y)
+    assert np.all(np.isfinite(got["2"]))
+    np.testing.assert_array_equal(bits(got["2"]), bits(got["0"]))
+    assert normwise(got["2"], O.gemm(W, Xq, n_out, n_in, n_tok, nthreads=16)) <= TOL
+
+
 def test_gemm_equals_gemv_per_token():
     case("gemm n_tok=3 equals three gemv")
     n_out, n_in, n_tok = 300, 5120, 3
