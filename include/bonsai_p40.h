@@ -324,17 +324,20 @@ int64_t bonsai_p40_chain_plan_bytes(int n_steps);
 // (and outside stream capture).  Errors: 1 if a step is invalid (nothing is
 // written), else the copy's hipError_t.
 int bonsai_p40_chain_plan(const bonsai_p40_chain_step * steps, int n_steps, void * plan);
-// Workspace of bonsai_p40_chain_run: one flag word per workgroup.  Zero-fill
-// it once before its first use and then leave it alone: every completed
-// launch leaves it ready for the next.  Launches that may run at the same time
-// need their own workspaces.
+// Workspace of bonsai_p40_chain_run: one flag word per workgroup and, in its
+// last word, the abort word.  Zero-fill it once before its first use and
+// then leave it alone: every completed launch leaves it ready for the next.
+// Launches that may run at the same time need their own workspaces.
 #define BONSAI_P40_CHAIN_WORKSPACE_BYTES 4096
 // Runs a planned chain on the device it was planned on.  status (device, may
-// be NULL): incremented once for every barrier wait that gave up (the chain's
+// be NULL): incremented for every barrier wait that gave up (the chain's
 // workgroups could not all be resident, e.g. beside another kernel); the
-// outputs of such a launch are not valid and the workspace must be
-// zero-filled again.  Errors: 1 on bad arguments, else the launch's
-// hipError_t.
+// first give-up sets the workspace's abort word, on which every workgroup
+// leaves at its next barrier or poll, so a failed launch ends within about
+// one wait bound.  The outputs of such a launch are not valid and the
+// workspace must be zero-filled again: a launch that finds the abort word
+// set adds 1 to status and does nothing.  Errors: 1 on bad arguments, else
+// the launch's hipError_t.
 int bonsai_p40_chain_run(const void * plan, int n_steps, void * workspace, uint32_t * status,
                          bonsai_stream stream);
 

@@ -6,20 +6,23 @@
 // a ramp (the first weight bytes arrive ~1 us after the workgroups start) and
 // a tail.  Here one workgroup per CU runs all steps:
 //   * between dependent phases every workgroup passes a grid-wide barrier: it
-//     publishes its barrier count in its own flag word (no atomics: a
-//     contended device-scope atomic is serialised at the memory side, ~0.7 us
-//     per operation while HBM streams) and wave 0 polls all flags, with a
-//     bounded number of polls (a wait that gives up is counted in *status);
+//     publishes its barrier count in its own flag word with an agent-scope
+//     release store (no read-modify-write: a contended device-scope atomic is
+//     serialised at the memory side, ~0.7 us per operation while HBM streams)
+//     and wave 0 polls all flags, then acquires at agent scope; the number of
+//     polls is bounded: a wait that gives up is counted in *status and sets
+//     the workspace's abort word, which every later barrier and poll checks,
+//     so every workgroup of a failed launch leaves within one wait bound;
 //   * before it waits, every wave but wave 0 already issues the LDS-DMA of its
 //     first weight units of the next GEMV step (the weights do not depend on
 //     the barrier), so HBM keeps streaming through the barrier;
 //   * wave 0 alone stores what other workgroups read (every wave's outputs
 //     reach it through LDS), with device-coherent stores (cache policy sc1),
 //     and never has weight DMAs in flight when it publishes its flag: one
-//     vmcnt(0) then covers exactly the workgroup's stores, and no L2
-//     write-back is needed;
-//   * inputs written in the launch are read with device-scope loads (sc1), so
-//     no cache invalidation is needed after a barrier;
+//     vmcnt(0) then covers exactly the workgroup's stores, and the release's
+//     L2 write-back finds none of them dirty;
+//   * inputs written in the launch are read with device-scope loads (sc1)
+//     after the barrier's acquire;
 //   * a step's descriptor is copied into registers while the wave has no DMA
 //     in flight (a descriptor load behind in-flight DMAs would wait for them).
 // Each step computes exactly what its per-launch entry point computes: the
@@ -43,7 +46,8 @@ constexpr int CW = 8;                // waves per workgroup
 constexpr int CD = 2;                // units in flight per wave in the steady state
 constexpr int CSL = CD + 1;          // ring slots per wave: also the prefetch depth
 constexpr int CPOL_SC1 = 16;         // cache policy sc1: device-scope coherent access
-constexpr int MAX_WG = BONSAI_P40_CHAIN_WORKSPACE_BYTES / 4;
+constexpr int MAX_WG = BONSAI_P40_CHAIN_WORKSPACE_BYTES / 4 - 1;   // flag words
+constexpr int ABORT_WORD = MAX_WG;   // the workspace's last word: set once a barrier wait gave up
 constexpr int GLUE_ONLY = 4;         // device step kind: a glue phase and no GEMV
 // polls of a barrier wait before it gives up (one device-coherent load round
 // plus a short sleep each: some tens of milliseconds in all)
@@ -110,29 +114,54 @@ __device__ __forceinline__ void store_sc1(void * p, uint32_t v) {
 }
 
 // Grid-wide barrier number `target` (the flags count barriers passed, across
-// launches), entered by all waves; wave 0 publishes and polls.
-__device__ void grid_barrier(uint32_t * flags, uint32_t target, uint32_t * status) {
+// launches), entered by all waves; wave 0 publishes and polls.  Returns false
+// when the launch is being abandoned: this workgroup's wait gave up (counted
+// in *status), or another workgroup's did (the abort word is set).
+__device__ bool grid_barrier(uint32_t * flags, uint32_t target, uint32_t * status) {
+    __shared__ uint32_t bar_ok;
     if (threadIdx.x < 64) {
         wait_vmcnt<0>();                           // this workgroup's stores are acknowledged
-        if (threadIdx.x == 0) store_sc1(&flags[blockIdx.x], target);
-        const int nwg = gridDim.x;
-        uint32_t polls = 0;
-        while (true) {
-            bool ok = true;
-            for (int i = threadIdx.x; i < nwg; i += 64) {
-                const uint32_t f = __hip_atomic_load(&flags[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                ok = ok && (int)(f - target) >= 0;
+        uint32_t * abort_w = flags + ABORT_WORD;
+        bool ok = __hip_atomic_load(abort_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0;
+        if (ok) {
+            // the release orders the step's outputs (written by this wave)
+            // before the flag for every workgroup that acquires it
+            if (threadIdx.x == 0)
+                __hip_atomic_store(&flags[blockIdx.x], target, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            const int nwg = gridDim.x;
+            uint32_t polls = 0;
+            while (true) {
+                bool all = true;
+                for (int i = threadIdx.x; i < nwg; i += 64) {
+                    const uint32_t f = __hip_atomic_load(&flags[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    all = all && (int)(f - target) >= 0;
+                }
+                if (__builtin_amdgcn_ballot_w64(!all) == 0) break;
+                if (__hip_atomic_load(abort_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+                    ok = false;
+                    break;
+                }
+                if (++polls > CHAIN_SPIN_LIMIT) {
+                    if (threadIdx.x == 0) {
+                        if (status != nullptr)
+                            __hip_atomic_fetch_add(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(abort_w, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                    ok = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
             }
-            if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
-            if (++polls > CHAIN_SPIN_LIMIT) {
-                if (threadIdx.x == 0 && status != nullptr)
-                    __hip_atomic_fetch_add(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
+            // pairs with the other workgroups' release stores: their outputs
+            // are visible to every wave of this workgroup after the s_barrier
+            if (ok) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         }
+        if (threadIdx.x == 0) bar_ok = ok ? 1u : 0u;
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    return bar_ok != 0;
 }
 
 // Unit numbering of the streaming GEMV (gemv_nb_kernel): grid-strided over
@@ -462,6 +491,13 @@ chain_kernel(const ChainStep * __restrict__ plan, const ChainHeader * __restrict
             __hip_atomic_fetch_add(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
+    // a launch on a workspace whose abort word is set (an earlier launch gave
+    // up and the workspace was not zero-filled again) does nothing
+    if (__hip_atomic_load(flags + ABORT_WORD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+        if (blockIdx.x == 0 && threadIdx.x == 0 && status != nullptr)
+            __hip_atomic_fetch_add(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     // every workgroup's flag equals the number of barriers the launches before
     // this one passed
     const uint32_t base = __hip_atomic_load(&flags[blockIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -472,7 +508,7 @@ chain_kernel(const ChainStep * __restrict__ plan, const ChainHeader * __restrict
     for (int d = 0; d < n_dev; ++d) {
         ChainStep nx;
         if (cur.glue) {
-            if (!first) grid_barrier(flags, base + (++nbar), status);
+            if (!first && !grid_barrier(flags, base + (++nbar), status)) break;
             first = false;
             glue_phase(cur, arena);
         }
@@ -480,7 +516,7 @@ chain_kernel(const ChainStep * __restrict__ plan, const ChainHeader * __restrict
             nx = load_step(plan, d + 1, n_dev);    // no prefetch into a glue-only step
             pf = 0;
         } else {
-            if (!first) grid_barrier(flags, base + (++nbar), status);
+            if (!first && !grid_barrier(flags, base + (++nbar), status)) break;
             first = false;
             if (cur.nb == 40) {
                 if (cur.kind == BONSAI_P40_CHAIN_Q8)

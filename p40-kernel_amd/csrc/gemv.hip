@@ -30,6 +30,9 @@
 #include "fwht_device.h"
 #include "gemv_device.h"
 #include "host_state.h"
+
+#include <atomic>
+#include <mutex>
 #include "../../include/bonsai_p40.h"
 
 #include <stdlib.h>
@@ -261,9 +264,11 @@ constexpr uint32_t EPI_SPIN_LIMIT = 1u << 16;
 // GEMVs).  Every workgroup read the generation word sync[1] when it started
 // (gen0: nothing advances it before every workgroup has taken its ticket),
 // stored its gate and up rows with device-coherent stores, waits for their
-// acknowledgement and takes one ticket from sync[0].  The workgroup holding the
-// last ticket zeroes sync[0] and then advances sync[1]: every row of both
-// matrices is in memory from then on.  The workgroups holding the last
+// acknowledgement and takes one ticket from sync[0] with an agent-scope
+// acquire-release read-modify-write (the tickets form one release sequence).
+// The workgroup holding the last ticket has thereby acquired every row of
+// both matrices; it zeroes sync[0] and then advances sync[1] with a release
+// store, which the finalisers acquire.  The workgroups holding the last
 // nfin = min(#workgroups, nblk) tickets are the finalisers: each waits
 // (bounded) for sync[1] to move past the value it read (the last one does
 // not wait), then finishes the 1024-blocks f, f + nfin, ...: SwiGLU of the
@@ -284,14 +289,16 @@ __device__ __forceinline__ void ffn_epilogue(const MatGroup & mg, float * h_lds,
     const uint32_t nwg = gridDim.x;
     const uint32_t nfin = nwg < (uint32_t)e.nblk ? nwg : (uint32_t)e.nblk;
     if (threadIdx.x == 0) {
-        const uint32_t t = __hip_atomic_fetch_add(&e.sync[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // release: this workgroup's rows (every wave's stores acknowledged
+        // above) before its ticket; acquire: the rows of every earlier ticket
+        const uint32_t t = __hip_atomic_fetch_add(&e.sync[0], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         uint32_t give = 0;
         if (t == nwg - 1) {
             // every workgroup's rows are acknowledged: reset the ticket counter
             // for the next launch (nothing reads it again in this one) and open
             // the finalisers' wait
             __hip_atomic_store(&e.sync[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&e.sync[1], gen0 + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&e.sync[1], gen0 + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         } else if (t >= nwg - nfin) {
             uint32_t polls = 0;
             while (__hip_atomic_load(&e.sync[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen0) {
@@ -301,6 +308,8 @@ __device__ __forceinline__ void ffn_epilogue(const MatGroup & mg, float * h_lds,
                 }
                 __builtin_amdgcn_s_sleep(1);
             }
+            // pairs with the last ticket holder's release store
+            if (!give) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         }
         epi_ticket = t;
         epi_gave_up = give;
@@ -313,7 +322,9 @@ __device__ __forceinline__ void ffn_epilogue(const MatGroup & mg, float * h_lds,
             __hip_atomic_fetch_add(e.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // every wave of a finaliser reads the rows after thread 0's acquire (the
+    // workgroup barrier above orders it)
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     for (int b = (int)(t - (nwg - nfin)); b < e.nblk; b += (int)nfin) {
         const float * g = mg.y[0] + (size_t)HBLK * b;
         const float * u = mg.y[1] + (size_t)HBLK * b;
@@ -1619,24 +1630,32 @@ struct ScratchAddr {
 };
 
 // device address of `scratch` on the calling thread's current device, looked
-// up once per device with that device current
+// up with that device current; only a successful lookup is kept (a failed one
+// is retried on the next call)
 ScratchAddr scratch_address() {
-    static pq2host::PerDeviceOnce once;
-    static ScratchAddr addr[pq2host::MAX_DEVICES];
+    static std::atomic<uint8_t *> addr[pq2host::MAX_DEVICES];
+    static std::mutex mu[pq2host::MAX_DEVICES];
+    ScratchAddr a;
     const int d = pq2host::current_device();
     if (d < 0 || d >= pq2host::MAX_DEVICES) {
-        ScratchAddr a;
         a.err = hipErrorInvalidDevice;
         return a;
     }
-    pq2host::once_per_device(once, [d] {
-        void * p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (e != hipSuccess) (void)hipGetLastError();
-        addr[d].err = e;
-        addr[d].ptr = e == hipSuccess ? static_cast<uint8_t *>(p) : nullptr;
-    });
-    return addr[d];
+    a.ptr = addr[d].load(std::memory_order_acquire);
+    if (a.ptr != nullptr) return a;
+    std::lock_guard<std::mutex> g(mu[d]);
+    a.ptr = addr[d].load(std::memory_order_relaxed);
+    if (a.ptr != nullptr) return a;
+    void * p = nullptr;
+    a.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (a.err != hipSuccess || p == nullptr) {
+        (void)hipGetLastError();
+        if (a.err == hipSuccess) a.err = hipErrorInvalidSymbol;
+        return a;
+    }
+    a.ptr = static_cast<uint8_t *>(p);
+    addr[d].store(a.ptr, std::memory_order_release);
+    return a;
 }
 
 }  // namespace

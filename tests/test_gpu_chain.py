@@ -180,3 +180,112 @@ def test_chain_glue_step_alone_and_first():
         assert int(ch.status.item()) == 0
         assert np.array_equal(bits(hq), bits(ref))
     assert np.array_equal(bits(y), bits(yref))
+
+
+def test_chain_gemv_then_glue_only_step():
+    """A GEMV step followed by a glue step that ends the chain (the device
+    plan's glue-only step after a GEMV), against the per-step launches."""
+    case("chain: RMSNorm+FWHT gate/up, then SwiGLU as the last step")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(13)
+    Wg, Wu = weights(gen, N_FF, N_EMBD), weights(gen, N_FF, N_EMBD)
+    x = torch.randn(N_EMBD, generator=gen, device="cuda")
+    nw = torch.rand(N_EMBD, generator=gen, device="cuda") + 0.5
+    s_gu, s_d = signs_vec(21, N_EMBD), signs_vec(22, N_FF)
+    rg, ru = f32(N_FF), f32(N_FF)
+    B.rmsnorm_fwht_gemv_group([Wg, Wu], x, nw, s_gu, [rg, ru], [N_FF, N_FF], N_EMBD, 1e-6)
+    rhq = torch.zeros(B.q8_bytes(N_FF), dtype=torch.uint8, device="cuda")
+    B.swiglu_fwht_quant(rg, ru, s_d, rhq, N_FF)
+    g, u = f32(N_FF), f32(N_FF)
+    hq = torch.zeros_like(rhq)
+    ch = B.Chain([B.chain_step(B.CHAIN_RMSNORM_FWHT, [Wg, Wu], [g, u], [N_FF, N_FF], N_EMBD, x=x, norm_w=nw,
+                               signs=s_gu, eps=1e-6),
+                  B.chain_step(B.CHAIN_SWIGLU, n_in=N_FF, x=g, x2=u, signs=s_d, q_out=hq)])
+    for launch in range(2):
+        hq.zero_()
+        ch.run()
+        assert int(ch.status.item()) == 0
+        assert np.array_equal(bits(g), bits(rg)) and np.array_equal(bits(u), bits(ru))
+        assert np.array_equal(bits(hq), bits(rhq)), f"launch {launch}: the glue-only step's bytes differ"
+
+
+def test_chain_two_glue_steps_in_a_row():
+    """gate/up, two SwiGLU glue steps in a row (the second with other signs),
+    then the down GEMV on the second one's output, against the per-step
+    launches."""
+    case("chain: gate/up, SwiGLU, SwiGLU, Q8 down")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(17)
+    Wg, Wu = weights(gen, N_FF, N_EMBD), weights(gen, N_FF, N_EMBD)
+    Wd = weights(gen, N_EMBD, N_FF)
+    x = torch.randn(N_EMBD, generator=gen, device="cuda")
+    xq = torch.empty(B.q8_bytes(N_EMBD), dtype=torch.uint8, device="cuda")
+    B.fwht_quant(x, None, xq, N_EMBD)
+    s1, s2 = signs_vec(31, N_FF), signs_vec(32, N_FF)
+    rg, ru, ry = f32(N_FF), f32(N_FF), f32(N_EMBD)
+    B.gemv_group([Wg, Wu], xq, [rg, ru], [N_FF, N_FF], N_EMBD)
+    rh1 = torch.zeros(B.q8_bytes(N_FF), dtype=torch.uint8, device="cuda")
+    rh2 = torch.zeros_like(rh1)
+    B.swiglu_fwht_quant(rg, ru, s1, rh1, N_FF)
+    B.swiglu_fwht_quant(rg, ru, s2, rh2, N_FF)
+    B.gemv(Wd, rh2, ry, N_EMBD, N_FF)
+    g, u, y = f32(N_FF), f32(N_FF), f32(N_EMBD)
+    h1, h2 = torch.zeros_like(rh1), torch.zeros_like(rh1)
+    ch = B.Chain([B.chain_step(B.CHAIN_Q8, [Wg, Wu], [g, u], [N_FF, N_FF], N_EMBD, x=xq),
+                  B.chain_step(B.CHAIN_SWIGLU, n_in=N_FF, x=g, x2=u, signs=s1, q_out=h1),
+                  B.chain_step(B.CHAIN_SWIGLU, n_in=N_FF, x=g, x2=u, signs=s2, q_out=h2),
+                  B.chain_step(B.CHAIN_Q8, [Wd], [y], [N_EMBD], N_FF, x=h2)])
+    for launch in range(2):
+        for t in (h1, h2):
+            t.zero_()
+        y.fill_(float("nan"))
+        ch.run()
+        assert int(ch.status.item()) == 0
+        assert np.array_equal(bits(h1), bits(rh1)) and np.array_equal(bits(h2), bits(rh2))
+        assert np.array_equal(bits(y), bits(ry)), f"launch {launch}: the down GEMV after two glue steps differs"
+
+
+def test_chain_barrier_give_up_is_sticky():
+    """A launch whose barrier waits cannot succeed ends within about one wait
+    bound.  Forced from the host: every workgroup's flag but one says 1000
+    barriers passed, so the others wait for a count that workgroup never
+    publishes; their bounded waits give up and set the abort word, on which
+    every workgroup leaves (every wave exits: nothing spins unbounded).  A
+    second launch on that workspace does nothing and counts 1."""
+    import time
+    case("chain: barrier give-up is sticky (forced from the host)")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(23)
+    layer = Layer(gen, False, 5)
+    x0 = torch.randn(N_EMBD, generator=gen, device="cuda")
+    steps, bufs = [], []                                # bufs keeps every output alive
+    for _ in range(4):                                  # 20 steps: about 20 barriers
+        bufs.append(layer.buffers())
+        steps += layer.steps(x0, bufs[-1], 1e-6)
+    ch = B.Chain(steps)
+    ch.run()                                             # a good launch first
+    torch.cuda.synchronize()
+    assert int(ch.status.item()) == 0
+    flags = ch.workspace.view(torch.int32)
+    n_wg = torch.cuda.get_device_properties(0).multi_processor_count
+    flags[:n_wg] = 1000
+    flags[3] = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ch.run()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    given_up = int(ch.status.item())
+    assert given_up >= 1, "no barrier wait gave up"
+    assert int(flags[-1].item()) == 1, "the abort word is not set"
+    # one wait bound is some tens of ms; without the abort word every later
+    # barrier would poll its full bound again (~20 x that)
+    assert dt < 1.0, f"the abandoned launch took {dt:.2f} s"
+    ch.run()                                             # the abort word is still set
+    torch.cuda.synchronize()
+    assert int(ch.status.item()) == given_up + 1
+    ch.workspace.zero_()                                 # zero-filled again: launches work
+    ch.status.zero_()
+    ch.run()
+    torch.cuda.synchronize()
+    assert int(ch.status.item()) == 0
