@@ -154,6 +154,19 @@ def bench_stream_read(nbytes, steps, warmup, blocks=8192):
     return ms
 
 
+def bench_unit_dma(n_out, n_in, steps, warmup, gen):
+    """bonsai_p40_unit_dma_probe: the decode GEMV's unit DMA schedule alone (no
+    activation, no arithmetic) over the same rotating weight copies as
+    bench_gemv -- the floor the GEMV's own addressing sets."""
+    W0 = synth_weights(n_out, n_in, gen)
+    R = copies_for(W0.numel())
+    Ws = [W0] + [W0.clone() for _ in range(R - 1)]
+    sink = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    ms = time_loop(lambda i: B.unit_dma_probe(Ws[i % R], n_out, n_in, sink), steps, warmup)
+    del Ws
+    return ms
+
+
 def bench_fwht_gemv(n_out, n_in, steps, warmup, gen):
     """bonsai_p40_fwht_gemv: FWHT + Q8_1 of an fp32 activation and the GEMV in
     one launch, over rotating weight copies."""
@@ -567,6 +580,8 @@ def main():
                     help="time Python launches one by one instead of replaying HIP graphs")
     ap.add_argument("--only-read", action="store_true",
                     help="stream-read probe over 23,750,272-byte buffers only (PMC calibration)")
+    ap.add_argument("--shape", default=f"{N_FF}x{N_EMBD}", metavar="ROWSxCOLS",
+                    help="matrix of --only-gemm / --only-small (default the headline 17408x5120)")
     ap.add_argument("--only-gemm", type=int, default=0, metavar="M",
                     help="prefill GEMM 17408x5120 with M tokens only (profiling)")
     ap.add_argument("--only-small", type=int, default=0, metavar="B",
@@ -609,13 +624,14 @@ def main():
 
     if args.only_gemm or args.only_small:
         m = args.only_gemm or args.only_small
-        ms = bench_gemv(N_FF, N_EMBD, args.steps, args.warmup, gen, n_tok=m)
+        no, ni = map(int, args.shape.split("x"))
+        ms = bench_gemv(no, ni, args.steps, args.warmup, gen, n_tok=m)
         if args.only_gemm:
-            tops = 2.0 * m * N_FF * N_EMBD / (ms * 1e-3) / 1e12
-            print(f"[bench] gemm 17408x5120 M={m}: {ms * 1e3:.1f} us  {tops:.1f} TOPS", file=sys.stderr, flush=True)
+            tops = 2.0 * m * no * ni / (ms * 1e-3) / 1e12
+            print(f"[bench] gemm {no}x{ni} M={m}: {ms * 1e3:.1f} us  {tops:.1f} TOPS", file=sys.stderr, flush=True)
         else:
-            gbs = gemv_bytes(N_FF, N_EMBD, m) / (ms * 1e-3) / 1e9
-            print(f"[bench] small batch 17408x5120 B={m}: {ms * 1e3:.2f} us  {gbs:.1f} GB/s", file=sys.stderr, flush=True)
+            gbs = gemv_bytes(no, ni, m) / (ms * 1e-3) / 1e9
+            print(f"[bench] small batch {no}x{ni} B={m}: {ms * 1e3:.2f} us  {gbs:.1f} GB/s", file=sys.stderr, flush=True)
         return
 
     if args.only_sweep:
@@ -660,6 +676,15 @@ def main():
                                        "note": "plain 16-byte streaming read of 23,750,272 B per launch: "
                                                "the achievable ceiling for one launch of this size"}
     print(f"[bench] stream read ceiling: {extra['stream_read_same_bytes']}", file=sys.stderr, flush=True)
+    for (no, ni) in ((N_FF, N_EMBD), (N_EMBD, N_FF)):
+        ms_dma = bench_unit_dma(no, ni, args.steps, args.warmup, gen)
+        nb_ = B.pq2_bytes(no, ni)
+        extra[f"gemv_unit_dma_skeleton_{no}x{ni}"] = {
+            "us": round(ms_dma * 1e3, 3), "GB/s": round(nb_ / (ms_dma * 1e-3) / 1e9, 1),
+            "note": "bonsai_p40_unit_dma_probe: the GEMV's own weight DMA schedule (units, grid, ring, waits) "
+                    "with no activation and no arithmetic"}
+        print(f"[bench] unit DMA skeleton {no}x{ni}: {extra[f'gemv_unit_dma_skeleton_{no}x{ni}']}",
+              file=sys.stderr, flush=True)
     sb, sms = bench_sustained_read()
     sus_gbs = sb / (sms * 1e-3) / 1e9
     extra["stream_read_sustained"] = {"bytes": sb, "us": round(sms * 1e3, 1), "GB/s": round(sus_gbs, 1),

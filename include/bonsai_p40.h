@@ -384,6 +384,17 @@ int bonsai_p40_mfma_probe(int kind, int blocks, int iters, uint64_t * clk, uint3
 // arguments.
 int bonsai_p40_overlap_probe(int mode, int nf, int blocks, int iters, uint32_t * sink, bonsai_stream stream);
 
+// Measurement helper: the decode GEMV's weight stream alone -- the unit
+// LDS-DMA schedule bonsai_p40_gemv runs for an n_out x n_in PQ2_0 matrix
+// (n_in 5120 or 17408; same units, grid, wave numbering, ring depth, issue
+// rounds and waits), with no activation and no arithmetic: the floor the
+// GEMV's own addressing puts under it (the role of the reference's
+// tools/bwtest.cu:70-90).  W 4-byte aligned, under 2 GiB; sink needs one word
+// per CU and is written only in a practically impossible case.  Errors: 1 on
+// other widths, bad sizes or alignment.
+int bonsai_p40_unit_dma_probe(const void * W, int64_t n_out, int64_t n_in, uint32_t * sink,
+                              bonsai_stream stream);
+
 // Measurement: one empty kernel (`blocks` workgroups of `threads` threads,
 // 1..1024); replayed back to back it gives the cost of a launch that waits for
 // the one before it -- the floor under every kernel of a decode chain.

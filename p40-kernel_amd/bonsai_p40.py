@@ -59,6 +59,7 @@ SIGNATURES = {
     "bonsai_p40_mfma_probe": [C.c_int, C.c_int, C.c_int, _V, _V, _V],
     "bonsai_p40_overlap_probe": [C.c_int, C.c_int, C.c_int, C.c_int, _V, _V],
     "bonsai_p40_launch_probe": [C.c_int, C.c_int, _V, _V],
+    "bonsai_p40_unit_dma_probe": [_V, _I64, _I64, _V, _V],
     "bonsai_p40_chain_plan_bytes": [C.c_int],
     "bonsai_p40_chain_plan": [_V, C.c_int, _V],
     "bonsai_p40_chain_run": [_V, C.c_int, _V, _V, _V],
@@ -315,6 +316,10 @@ def overlap_probe(mode: int, nf: int, blocks: int, iters: int, sink, stream=None
 
 def launch_probe(blocks: int, threads: int, sink, stream=None) -> None:
     _check("bonsai_p40_launch_probe", call("bonsai_p40_launch_probe", blocks, threads, sink, stream=stream))
+
+
+def unit_dma_probe(W, n_out: int, n_in: int, sink, stream=None) -> None:
+    _check("bonsai_p40_unit_dma_probe", call("bonsai_p40_unit_dma_probe", W, n_out, n_in, sink, stream=stream))
 
 
 def stream_read(buf, nbytes: int, out, blocks: int, stream=None) -> None:

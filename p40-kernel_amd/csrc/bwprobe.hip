@@ -9,8 +9,13 @@
 //    clock and real-time counters read around its loop so the host can derive
 //    the clock the MFMAs ran at;
 //  * VALU / MFMA overlap: the same MFMAs with and without independent fp32
-//    FMAs in the same wave stream.
-#include "pq2_device.h"
+//    FMAs in the same wave stream;
+//  * the decode GEMV's weight stream alone (the analog of the reference's
+//    GEMV-addressing read, tools/bwtest.cu:70-90): the unit LDS-DMA schedule
+//    of gemv_nb_kernel (same units, grid, wave numbering, ring depth, issue
+//    rounds and waits) with no activation and no arithmetic.
+#include "gemv_device.h"
+#include "host_state.h"
 #include "../../include/bonsai_p40.h"
 
 namespace {
@@ -176,6 +181,61 @@ gemm_core_probe_kernel(int iters, uint32_t * __restrict__ sink) {
     if (z == 1234.5f) sink[blockIdx.x] = 1u;       // practically never: keeps the work live
 }
 
+// The GEMV's unit DMA alone.  Units of G rows are dealt to the grid's waves
+// grid-strided with the GEMV's XCD-grouped numbering; each wave keeps D units
+// in flight in a ring of D + 1 LDS slots: wait for unit i, issue unit i + D,
+// and do nothing with the bytes.  Issue rounds are separated by workgroup
+// barriers as in the GEMV.  Wave 0 folds one word of its last unit into a
+// sink word that is written only in a practically impossible case.
+template <int NB, int D, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES)
+unit_dma_probe_kernel(const uint8_t * __restrict__ W, int n_out, int units_per_wave, int xcd_log2m,
+                      uint32_t * __restrict__ sink) {
+    using P = pq2::NbSpec<NB>;
+    constexpr int SL = D + 1;
+    __shared__ __attribute__((aligned(16))) uint8_t ring_all[WAVES][SL][P::LDSB];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint8_t (*ring)[P::LDSB] = ring_all[wave];
+    const int n_units = (n_out + P::G - 1) / P::G;
+    int gw = wave * gridDim.x + blockIdx.x;
+    if (xcd_log2m > 0) {
+        const int K = gridDim.x >> 3;
+        const int t = wave * K + (blockIdx.x >> 3);
+        const int m = (1 << xcd_log2m) - 1;
+        gw = (((t >> xcd_log2m) << 3) + (blockIdx.x & 7)) << xcd_log2m | (t & m);
+    }
+    const int NW = gridDim.x * WAVES;
+    const int nu = gw < n_units ? min(units_per_wave, (n_units - 1 - gw) / NW + 1) : 0;
+    const int m_bytes = n_out * pq2::PQ2_BYTES * NB;
+    uint32_t poff[P::NPL];
+#pragma unroll
+    for (int k = 0; k < P::NPL; ++k) poff[k] = 16u * (uint32_t)min(lane + 64 * k, P::NPIECE - 1);
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+        __builtin_amdgcn_s_barrier();
+        if (nu > 0)
+            pq2::unit_buffer_dma<P::NPL>(W, m_bytes, (uint32_t)(gw + min(i, nu - 1) * NW) * (uint32_t)P::UB, poff,
+                                         ring[i]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int i = 0; i < nu; ++i) {
+        const int newer = min(D - 1, nu - 1 - i);
+        if (newer >= 2) pq2::wait_vmcnt<2 * P::NPL>();
+        else if (newer == 1) pq2::wait_vmcnt<P::NPL>();
+        else pq2::wait_vmcnt<0>();
+        __builtin_amdgcn_wave_barrier();
+        if (i + D < nu)
+            pq2::unit_buffer_dma<P::NPL>(W, m_bytes, (uint32_t)(gw + (i + D) * NW) * (uint32_t)P::UB, poff,
+                                         ring[(i + D) % SL]);
+    }
+    pq2::wait_vmcnt<0>();
+    if (nu > 0 && lane == 0 && wave == 0) {
+        const uint32_t v = *reinterpret_cast<const uint32_t *>(&ring[(nu - 1) % SL][0]);
+        if (v == 0x9e3779b9u && n_out < 0) sink[blockIdx.x] = v;   // never: n_out > 0
+    }
+}
+
 // An empty kernel: the cost of a launch that depends on the one before it.
 __global__ void __launch_bounds__(1024) empty_probe_kernel(uint32_t * __restrict__ sink) {
     if (threadIdx.x == 0x7fffffff) sink[0] = 1u;    // never
@@ -223,6 +283,46 @@ extern "C" int bonsai_p40_launch_probe(int blocks, int threads, uint32_t * sink,
     hipLaunchKernelGGL(empty_probe_kernel, dim3((unsigned)blocks), dim3((unsigned)threads), 0, (hipStream_t)stream,
                        sink);
     return (int)hipGetLastError();
+}
+
+namespace {
+
+// the GEMV's launch geometry for the probe's two row widths: 5120 columns (2-row
+// units, one 8-wave workgroup per CU, ring depth 2) and 17408 columns (1-row
+// units, one 4-wave workgroup per CU, ring depth 2); grid, units per wave and
+// XCD grouping follow the GEMV's dispatcher for a single matrix
+template <int NB, int D, int WAVES>
+int launch_unit_dma_probe(const uint8_t * W, int n_out, uint32_t * sink, hipStream_t st) {
+    using P = pq2::NbSpec<NB>;
+    const int n_units = (n_out + P::G - 1) / P::G;
+    int blocks = pq2host::device_info().cus;
+    const int max_blocks = (n_units + WAVES - 1) / WAVES;
+    if (blocks > max_blocks) blocks = max_blocks;
+    const int NW = blocks * WAVES;
+    int upw = (n_units + NW - 1) / NW;
+    if (upw > 64 / P::G) {
+        upw = 64 / P::G;
+        blocks = (n_units + upw * WAVES - 1) / (upw * WAVES);
+    }
+    int xl = 3;
+    if (blocks % 8 != 0) xl = 0;
+    while (xl > 0 && ((blocks / 8) * WAVES) % (1 << xl) != 0) --xl;
+    hipLaunchKernelGGL((unit_dma_probe_kernel<NB, D, WAVES>), dim3(blocks), dim3(64 * WAVES), 0, st, W, n_out, upw,
+                       xl, sink);
+    return (int)hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" int bonsai_p40_unit_dma_probe(const void * W, int64_t n_out, int64_t n_in, uint32_t * sink,
+                                         bonsai_stream stream) {
+    if (W == nullptr || sink == nullptr || n_out <= 0 || ((uintptr_t)W & 3u) != 0) return 1;
+    if (n_in != 5120 && n_in != 17408) return 1;
+    if (n_out * (n_in / 128) * 34 >= 0x80000000ll) return 1;
+    const hipStream_t st = (hipStream_t)stream;
+    const uint8_t * w = static_cast<const uint8_t *>(W);
+    if (n_in == 5120) return launch_unit_dma_probe<40, 2, 8>(w, (int)n_out, sink, st);
+    return launch_unit_dma_probe<136, 2, 4>(w, (int)n_out, sink, st);
 }
 
 extern "C" int bonsai_p40_stream_read(const void * buf, int64_t bytes, uint32_t * out, int blocks,

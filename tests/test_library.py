@@ -73,6 +73,9 @@ NULL = None
     ("bonsai_p40_launch_probe", (1, 2048, 16), 1),
     ("bonsai_p40_launch_probe", (1, 64, NULL), 1),
     ("bonsai_p40_overlap_probe", (4, 1, 1, 1, 16), 1),                 # no mode 4
+    ("bonsai_p40_unit_dma_probe", (16, 16, 4096, 16), 1),              # not a GEMV width it models
+    ("bonsai_p40_unit_dma_probe", (16, 0, 5120, 16), 1),               # no rows
+    ("bonsai_p40_unit_dma_probe", (18, 16, 5120, 16), 1),              # W alignment
     ("bonsai_p40_gemv_group", (NULL, NULL, NULL, 1, NULL, 128), 1),   # NULL arrays
     ("bonsai_p40_fwht_gemv_group", (NULL, NULL, NULL, 1, 16, NULL, 1024), 1),
     ("bonsai_p40_rmsnorm_fwht_quant", (16, 16, NULL, 16, 1000, 1, C.c_float(1e-6)), 1),   # n % 1024
@@ -144,6 +147,7 @@ NULL_CASES = [
     ("bonsai_p40_quantize_pq2_0", (A, A, 128), (0, 1)),
     ("bonsai_p40_dequantize_pq2_0", (A, A, 128), (0, 1)),
     ("bonsai_p40_stream_read", (A, 1024, A, 1), (0, 2)),
+    ("bonsai_p40_unit_dma_probe", (A, 1024, 5120, A), (0, 3)),
 ]
 
 
