@@ -377,11 +377,18 @@ __device__ __forceinline__ void ffn_epilogue(const MatGroup & mg, float * h_lds,
 // unit p*nb + b = the 8 code bytes of chunk p of block b): the DMA moves the
 // same rows, only the lane's LDS offsets change (8-byte aligned code words,
 // no realignment).
+// whether a variant can run the shared tail (two 1 KiB DMA areas per ring
+// slot, the plain single-token unit layout)
+template <int NB, int NT, bool RP, bool DUMP, bool EPI>
+constexpr bool nb_tail_ok() {
+    return NT == 1 && !RP && !DUMP && !EPI && NbSpec<NB, NT>::LDSB >= 2048 && NbSpec<NB, NT>::S <= 16;
+}
+
 template <int NB, int D, int WAVES, bool DUMP, int ROT = 0, bool GROUP = false, int NT = 1, bool RP = false,
           bool RMS = false, bool OVL = false, bool EPI = false>
 __global__ void __launch_bounds__(64 * WAVES)
 gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * __restrict__ signs,
-               int32_t * __restrict__ dump, int units_per_wave, int n_tok, int xcd_log2m) {
+               int32_t * __restrict__ dump, int units_per_wave, int n_tok, int xcd_log2m, int tail) {
     using P = NbSpec<NB, NT>;
     static_assert(NT == 1 || (!DUMP && ROT == 0 && !GROUP), "small batch: plain GEMV only");
     static_assert(!RP || (NT == 1 && !GROUP && !DUMP), "repacked layout: single-token GEMV only");
@@ -417,15 +424,29 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
     // of NW units, groups of M = 2^xcd_log2m consecutive units go to one XCD
     // (its waves numbered wave-major), groups round-robin over the XCDs -- a
     // line shared by two neighbouring units is then fetched into one L2.
-    int gw = wave * gridDim.x + blockIdx.x;
-    if (xcd_log2m > 0) {
+    auto wave_index = [&](int w) {
+        if (xcd_log2m <= 0) return w * (int)gridDim.x + (int)blockIdx.x;
         const int K = gridDim.x >> 3;
-        const int t = wave * K + (blockIdx.x >> 3);
+        const int t = w * K + (blockIdx.x >> 3);
         const int m = (1 << xcd_log2m) - 1;
-        gw = (((t >> xcd_log2m) << 3) + (blockIdx.x & 7)) << xcd_log2m | (t & m);
-    }
+        return (((t >> xcd_log2m) << 3) + (int)(blockIdx.x & 7)) << xcd_log2m | (t & m);
+    };
+    const int gw = wave_index(wave);
     const int NW = gridDim.x * WAVES;
-    const int nu = gw < n_units ? min(units_per_wave, (n_units - 1 - gw) / NW + 1) : 0;
+    int nu = gw < n_units ? min(units_per_wave, (n_units - 1 - gw) / NW + 1) : 0;
+    // Shared tail (tail = T > 0, set by the dispatcher only when the last
+    // round of units is exactly the last units of waves 0..T-1 of every
+    // workgroup and every wave has at least D + 1 units): those T units leave
+    // their waves' loops; their T * S slots are dealt over all the
+    // workgroup's waves (slot q = k S + j of tail unit k to wave q % WAVES).
+    // Each wave DMAs its slots (one 544-byte slot per instruction) ahead of
+    // its first unit and computes their chunk dots while its first units
+    // land, keeping the products (dw, da s) in registers; after the loops the
+    // products meet in LDS and wave k folds unit k's slots in slot order with
+    // the loop's own FMA sequence -- y is bit-identical to the
+    // one-wave-per-unit schedule, and no wave carries a whole extra unit.
+    const int T = nb_tail_ok<NB, NT, RP, DUMP, EPI>() ? tail : 0;
+    if (T > 0 && wave < T) --nu;
     // EPI: the launch's generation, read at the start (its latency hides
     // behind the first loads; only thread 0 of the workgroup uses it)
     uint32_t epi_gen0 = 0;
@@ -533,6 +554,26 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
             __builtin_amdgcn_global_load_lds(src, (lds_void *)(&ring[slot][1024 * k]), 16, 0, CPOL_NT);
         }
     };
+    // shared tail: this wave's (up to two) tail slots, one DMA instruction
+    // each into ring slot D (free until step 0 issues unit D into it), older
+    // than every unit; an instruction without a slot reads past the buffer
+    // range (zeros, no memory traffic)
+    if (T > 0) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int q = wave + WAVES * r;
+            const int k = q < T * P::S ? q / P::S : 0;
+            const uint8_t * Wm;
+            float * ym;
+            int n_out_m, lu;
+            gs.at(wave_index(k) + (units_per_wave - 1) * NW, Wm, ym, n_out_m, lu);
+            const uint32_t m_bytes = (uint32_t)n_out_m * (uint32_t)(PQ2_BYTES * NB);
+            uint32_t off = m_bytes;
+            if (q < T * P::S && lane < SLOT_BYTES / 16)
+                off = (uint32_t)lu * (uint32_t)P::UB + (uint32_t)(SLOT_BYTES * (q - k * P::S) + 16 * lane);
+            tail_slot_dma(Wm, m_bytes, off, &ring[D][1024 * r]);
+        }
+    }
     // issue rounds: every wave's activation share, then every wave's first
     // unit, then every second unit, ...  A CU serves its requests roughly in
     // issue order, so the barrier between rounds keeps each wave's first
@@ -670,6 +711,42 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
     }
     float ykeep = 0.0f;                       // lane (G i + r) NT + t keeps row r, token t of unit i
 
+    float2 tail_e[2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+    if (T > 0) {
+        // shared tail: chunk dots of this wave's tail slots (landed: every
+        // unit DMA is younger); products (dw, da s) of slot r in tail_e[r]
+        wait_vmcnt<D * P::NPL>();
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int q = wave + WAVES * r;
+            if (q < T * P::S) {
+                const int j = q % P::S;
+                const uint8_t * tb = &ring[D][1024 * r];
+                const uint32_t * cpa = reinterpret_cast<const uint32_t *>(tb + cw_al);
+                const uint32_t w0 = __builtin_amdgcn_alignbyte(cpa[1], cpa[0], sh);
+                const uint32_t w1 = __builtin_amdgcn_alignbyte(cpa[2], cpa[1], sh);
+                const uint32_t dwb = *reinterpret_cast<const uint16_t *>(tb + dwo);
+                int s = 0;
+                float daj = 0.0f;
+#pragma unroll
+                for (int jj = 0; jj < P::S; ++jj) {
+                    if (jj == j) {
+                        s = chunk_dot_nib(w0, w1, ah[0][jj], al[0][jj], bias[0][jj]);
+                        daj = da[0][jj];
+                    }
+                }
+                float dw = f16_bits_to_f32(dwb);
+                if (P::PARTIAL && j == P::S - 1) dw = lane < 32 ? dw : 0.0f;
+                tail_e[r].x = dw;
+                tail_e[r].y = daj * (float)s;
+            }
+        }
+        // ring slot D is read out before step 0 DMAs unit D into it
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
+    }
+
     int i = 0;
     if (nu > 0) do {
         const int slot = i % SL;
@@ -738,6 +815,46 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         __builtin_amdgcn_s_waitcnt(0xC07F);        // lgkmcnt(0): this slot's reads are done
         __builtin_amdgcn_wave_barrier();
     } while (++i < nu);
+    if (T > 0) {
+        // the products of slot r to bytes 512 r + 8 lane of ring slot
+        // (nu + 1) % SL (free: its last unit was nu - D or earlier)
+        const int pslot = (nu + 1) % SL;
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+            if (wave + WAVES * r < T * P::S)
+                *reinterpret_cast<float2 *>(&ring[pslot][512 * r + 8 * lane]) = tail_e[r];
+        __builtin_amdgcn_s_waitcnt(0xC07F);        // lgkmcnt(0): this wave's products are in LDS
+        __builtin_amdgcn_s_barrier();
+        if (wave < T) {
+            // fold tail unit k = wave exactly as the loop folds a unit
+            const int k = wave;
+            float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+            for (int j = 0; j < P::S; ++j) {
+                const int q = k * P::S + j;
+                const float2 e = *reinterpret_cast<const float2 *>(
+                    &ring_all[q % WAVES][pslot][512 * (q / WAVES) + 8 * lane]);
+                if (P::G == 1 || j < P::SPLIT) acc0 = fmaf(e.x, e.y, acc0);
+                else if (j > P::SPLIT) acc1 = fmaf(e.x, e.y, acc1);
+                else if (lane < 32) acc0 = fmaf(e.x, e.y, acc0);
+                else acc1 = fmaf(e.x, e.y, acc1);
+            }
+            float t0, t1 = 0.0f;
+            if (P::G == 2) {
+                const float v = wave_sum2_to_lanes31_63(acc0, acc1);
+                t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+                t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+            } else {
+                t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_to_lane63(acc0)), 63));
+            }
+            const uint8_t * Wm;
+            float * ym;
+            int n_out_m, lu;
+            gs.at(gw + (units_per_wave - 1) * NW, Wm, ym, n_out_m, lu);
+            const int row = lu * P::G + lane;
+            if (lane < P::G && row < n_out_m) ym[row] = lane == 0 ? t0 : t1;
+        }
+    }
     if (!DUMP && lane < nu * P::G * NT) {
         const uint8_t * Wm;
         float * ym;
@@ -898,37 +1015,52 @@ int launch_nb_t(MatGroup mg, int n_mat, const void * xin, const float * signs, i
     int xl = knob(pq2host::K_GEMV_XCD_LOG2M, 3);
     if (xl < 0 || xl > 3 || blocks % 8 != 0) xl = 0;
     while (xl > 0 && ((blocks / 8) * WAVES) % (1 << xl) != 0) --xl;
+    // shared tail: the last round of L units must be exactly the last units of
+    // waves 0..T-1 of every workgroup -- L = T * blocks, and with the XCD
+    // numbering 2^xl must divide T * blocks / 8 (then unit index < L holds
+    // exactly for waves < T) -- and every wave keeps D + 1 or more units
+    int tail = 0;
+    if (nb_tail_ok<NB, NT, RP, DUMP, EPI>() && knob(pq2host::K_GEMV_TAIL, 0) != 0 && upw >= D + 1) {
+        const int nw = blocks * WAVES;
+        const int L = n_units - (upw - 1) * nw;
+        bool small = true;
+        for (int m = 0; m < n_mat; ++m) small = small && (int64_t)mg.n_out[m] * PQ2_BYTES * NB < 0x80000000ll;
+        if (small && L > 0 && L < nw && L % blocks == 0) {
+            const int T = L / blocks;
+            if (T * P::S <= 2 * WAVES && (xl == 0 || (T * (blocks / 8)) % (1 << xl) == 0)) tail = T;
+        }
+    }
     if constexpr (EPI) {
         static_assert(!OVL && !RP && NT == 1 && !DUMP, "FFN epilogue: the fused gate/up group");
         if (n_mat != 2) return 1;
         hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, ROT, true, 1, false, RMS, false, true>),
-                           dim3(blocks), dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl);
+                           dim3(blocks), dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl, tail);
     } else if constexpr (OVL) {
         if (n_mat > 1)
             hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, ROT, true, 1, false, false, true>), dim3(blocks),
-                               dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl);
+                               dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl, tail);
         else
             hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, ROT, false, 1, false, false, true>), dim3(blocks),
-                               dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl);
+                               dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl, tail);
     } else if constexpr (RMS) {
         if (n_mat > 1)
             hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, ROT, true, 1, false, true>), dim3(blocks),
-                               dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl);
+                               dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl, tail);
         else
             hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, ROT, false, 1, false, true>), dim3(blocks),
-                               dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl);
+                               dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl, tail);
     } else if constexpr (RP)
         hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, ROT, false, 1, true>), dim3(blocks),
-                           dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl);
+                           dim3(64 * WAVES), 0, st, mg, xin, signs, dump, upw, 1, xl, tail);
     else if constexpr (NT > 1)
         hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, false, 0, false, NT>), dim3(blocks), dim3(64 * WAVES),
-                           0, st, mg, xin, signs, dump, upw, n_tok, xl);
+                           0, st, mg, xin, signs, dump, upw, n_tok, xl, tail);
     else if (n_mat > 1)
         hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, DUMP, ROT, true>), dim3(blocks), dim3(64 * WAVES), 0,
-                           st, mg, xin, signs, dump, upw, 1, xl);
+                           st, mg, xin, signs, dump, upw, 1, xl, tail);
     else
         hipLaunchKernelGGL((gemv_nb_kernel<NB, D, WAVES, DUMP, ROT, false>), dim3(blocks), dim3(64 * WAVES), 0,
-                           st, mg, xin, signs, dump, upw, 1, xl);
+                           st, mg, xin, signs, dump, upw, 1, xl, tail);
     return (int)hipGetLastError();
 }
 

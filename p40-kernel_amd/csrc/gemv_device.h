@@ -60,6 +60,15 @@ __device__ __forceinline__ void unit_buffer_dma(const uint8_t * W, int m_bytes, 
                                                  CPOL_NT);
 }
 
+// One 16-byte LDS-DMA piece per lane from byte `off` of a buffer of m_bytes
+// bytes into dst + 16 lane; an offset at or past m_bytes lands zeros without
+// a memory access.
+__device__ __forceinline__ void tail_slot_dma(const uint8_t * W, uint32_t m_bytes, uint32_t off, uint8_t * dst) {
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(W), (short)0, (int)m_bytes, BUF_DW3);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void *)dst, 16, off, 0, 0, CPOL_NT);
+}
+
 // Reduce acc0 over lanes 0..63 and acc1 over lanes 0..63 at once:
 // v_permlane32_swap folds the upper half of acc0 onto its lower half and the
 // lower half of acc1 onto its upper half in one exchange, then one DPP tree

@@ -661,6 +661,65 @@ def test_gemv_xcd_unit_numbering(n_out, n_in, xl, knobs):
     np.testing.assert_array_equal(bits(got), bits(host(y0)))
 
 
+# rows of 5120 columns: 2-row units over 2048 waves (one 8-wave workgroup per
+# CU), so the last round holds T = 1..4 units per workgroup on these shapes;
+# 17407 rows end in a one-row unit inside the tail, 17000 rows leave a last
+# round that is not a whole number per workgroup (no shared tail)
+@pytest.mark.parametrize("xl", ["0", "3"])
+@pytest.mark.parametrize("n_out", [16896, 17407, 17408, 17920, 18432, 17000])
+def test_gemv_shared_tail(n_out, xl, knobs):
+    """The shared tail (the last round's units dealt slot by slot over every
+    wave of the workgroup) is bit-identical to one wave per unit, and both
+    match the oracle."""
+    n_in = 5120
+    case(f"gemv {n_out}x{n_in} shared tail, XCD group 2^{xl}")
+    W, xq = make(n_out, n_in, 3300 + n_out)
+    Wd, xd = dev(W), dev(xq)
+    knobs.set("BONSAI_GEMV_XCD_LOG2M", xl)
+    out = {}
+    for tail in ("1", "0"):
+        knobs.set("BONSAI_GEMV_TAIL", tail)
+        y = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+        B.gemv(Wd, xd, y, n_out, n_in)
+        out[tail] = host(y)
+    np.testing.assert_array_equal(bits(out["1"]), bits(out["0"]))
+    assert normwise(out["1"], O.gemv(W, xq, n_out, n_in, nthreads=16)) <= TOL
+
+
+@pytest.mark.parametrize("kind", ["group_gate_up", "group_qkv", "fwht", "rms_group"])
+def test_gemv_shared_tail_fused_and_grouped(kind, knobs):
+    """The shared tail in the grouped (gate+up: T = 4; q/k/v on 6-wave
+    workgroups: T = 2), fused-rotation and RMSNorm-fused launches: bit-identical
+    to one wave per unit."""
+    n_in = 5120
+    n_outs = {"group_gate_up": [17408, 17408], "group_qkv": [5120, 1024, 1024]}.get(kind, [17408])
+    case(f"shared tail {kind} {n_outs}x{n_in}")
+    Ws = [O.gen_weights(3400 + i, n, n_in) for i, n in enumerate(n_outs)]
+    Wd = [dev(W) for W in Ws]
+    x = O.gen_normal(3410, n_in)
+    xq = dev(O.quantize_q8_1(O.fwht(x), True))
+    signs = dev(np.where(O.gen_normal(3411, n_in) < 0, -1.0, 1.0).astype(np.float32))
+    nw = dev(O.gen_normal(3412, n_in) * 0.1 + 1)
+    out = {}
+    for tail in ("1", "0"):
+        knobs.set("BONSAI_GEMV_TAIL", tail)
+        ys = [torch.full((n,), float("nan"), dtype=torch.float32, device="cuda") for n in n_outs]
+        if kind.startswith("group"):
+            B.gemv_group(Wd, xq, ys, n_outs, n_in)
+        elif kind == "fwht":
+            B.fwht_gemv(Wd[0], dev(x), signs, ys[0], n_outs[0], n_in)
+        else:
+            B.rmsnorm_fwht_gemv_group(Wd, dev(x), nw, signs, ys, n_outs, n_in, 1e-6)
+        out[tail] = [host(y) for y in ys]
+    for a, b in zip(out["1"], out["0"]):
+        assert not np.isnan(a).any()
+        np.testing.assert_array_equal(bits(a), bits(b))
+    if kind.startswith("group"):
+        xqh = O.quantize_q8_1(O.fwht(x), True)
+        for W, n, got in zip(Ws, n_outs, out["1"]):
+            assert normwise(got, O.gemv(W, xqh, n, n_in, nthreads=16)) <= TOL
+
+
 def test_gemm_subnormal_and_zero_block_scales():
     """Blocks whose fp16 scale is subnormal or zero (the prefill kernel
     multiplies the scale into its f16 operand)."""
@@ -1036,3 +1095,18 @@ def test_rmsnorm():
     B.rmsnorm(dev(x), dev(w), y, n_rows, n, 1e-6)
     ref = x / np.sqrt((x.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6) * w
     np.testing.assert_allclose(host(y), ref, rtol=2e-6, atol=1e-6)
+
+
+# ------------------------------------------------------------------ probes
+@pytest.mark.parametrize("n_out,n_in", [(17408, 5120), (5120, 17408), (300, 5120), (7, 17408)])
+def test_unit_dma_probe_runs(n_out, n_in):
+    """The GEMV's DMA-only skeleton runs to completion on the GEMV's shapes
+    (full grid and a grid smaller than the CU count) and leaves its sink
+    untouched."""
+    case(f"unit_dma_probe {n_out}x{n_in}")
+    W = torch.randint(0, 256, (n_out * (n_in // 128) * 34,), dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    for _ in range(3):
+        B.unit_dma_probe(W, n_out, n_in, sink)
+    torch.cuda.synchronize()
+    assert int(sink.abs().sum()) == 0
