@@ -267,3 +267,42 @@ def test_gemm_f16_weight_window_stays_in_w(n_out, nb, w_align):
     want1 = dword(O_ + 4)
     assert np.array_equal(cw0, want0)
     assert np.array_equal(cw1, want1)
+
+
+# ------------------------------------------------ GEMV unit numbering / tail
+def _gemv_wave_index(w, blk, blocks, xl):
+    """gemv_nb_kernel's wave numbering (csrc/gemv.hip, wave_index): plain
+    slot-major, or groups of 2^xl consecutive units per XCD."""
+    if xl <= 0:
+        return w * blocks + blk
+    K = blocks >> 3
+    t = w * K + (blk >> 3)
+    m = (1 << xl) - 1
+    return ((((t >> xl) << 3) + (blk & 7)) << xl) | (t & m)
+
+
+def _dispatch_xl(blocks, waves, xl=3):
+    """launch_nb_t's choice of the XCD group size for a grid."""
+    if blocks % 8 != 0:
+        return 0
+    while xl > 0 and ((blocks // 8) * waves) % (1 << xl) != 0:
+        xl -= 1
+    return xl
+
+
+@pytest.mark.parametrize("waves", [4, 6, 8])
+@pytest.mark.parametrize("blocks", [8, 16, 24, 64, 248, 256, 768])
+def test_gemv_numbering_and_shared_tail_condition(blocks, waves):
+    """The numbering is a permutation of the grid's waves, and wherever the
+    dispatcher enables the shared tail (L = T * blocks last-round units, 2^xl
+    dividing T * blocks / 8) the units of the last round are exactly the last
+    units of waves 0..T-1 of every workgroup -- the kernel's assumption."""
+    for want_xl in range(4):
+        xl = min(want_xl, _dispatch_xl(blocks, waves))
+        idx = np.array([[_gemv_wave_index(w, b, blocks, xl) for b in range(blocks)] for w in range(waves)])
+        assert sorted(idx.ravel().tolist()) == list(range(waves * blocks))
+        for T in range(1, waves):
+            if xl and (T * (blocks // 8)) % (1 << xl) != 0:
+                continue
+            owner = idx < T * blocks
+            assert np.array_equal(owner, np.arange(waves)[:, None] < T + np.zeros((1, blocks), dtype=int))
