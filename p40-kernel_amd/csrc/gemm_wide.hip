@@ -407,9 +407,10 @@ namespace pq2 {
 // Rows [0, rows) of the product that the wide kernel takes, and its tile
 // height (*mi = 8: 256 rows, 5: 160 rows): the whole 256-row tiles whose
 // 256 x 256 tiles fill whole rounds of the device's CUs (the caller runs the
-// remaining rows on the 128-row kernel), or every row on 160-row tiles where
-// those fill one round; 0 where the kernel's requirements do not hold or its
-// tiles would not fill a round.  force: every row whenever the requirements
+// remaining rows on the 128-row kernel), or, short of one round, every row on
+// 256- or 160-row tiles where one round of them holds at least 3/4 of a full
+// round's outputs; 0 where the kernel's requirements do not hold or its tiles
+// would fill too little of a round.  force: every row whenever the requirements
 // hold (tests; the BONSAI_GEMM_WIDE_MI knob picks the tile height there).
 int64_t gemm_wide_rows(const void * W, const void * Xq, int64_t n_out, int64_t n_tok, int nb, int cus, bool force,
                        int * mi) {
@@ -426,9 +427,16 @@ int64_t gemm_wide_rows(const void * W, const void * Xq, int64_t n_out, int64_t n
     // 256-row tiles over the rows whose tiles fill whole rounds
     const int64_t R = n_out / 256, rounds = R * T / cus;
     if (rounds >= 1) return std::min<int64_t>(R, rounds * cus / T) * 256;
-    // 160-row tiles where they fill one round (5120 rows x 2048 tokens)
-    const int64_t R5 = (n_out + 159) / 160;
-    if (R5 * T <= cus && 8 * R5 * T >= 7 * cus) {
+    // Less than one round: a round of wide tiles takes about the same time
+    // however many CUs it fills, so one pays where at least 3/4 of a full
+    // round's outputs are real (measured on MI355X, one process, us, LDS kernel
+    // -> wide: 17408x5120 M = 768 225 -> 181 (256 rows), M = 512 165 -> 138
+    // (160 rows), 6144x5120 M = 2048 189 -> 180 (256 rows); at 5/8 and below
+    // the LDS kernel stays faster: 17408x5120 M = 384 116 against 137,
+    // 5120x6144 M = 1024 126 against 160)
+    const int64_t outputs = n_out * n_tok;
+    if ((n_out + 255) / 256 * T <= cus && 4 * outputs >= 3 * (int64_t)cus * 256 * WB_N) return n_out;
+    if ((n_out + 159) / 160 * T <= cus && 4 * outputs >= 3 * (int64_t)cus * 160 * WB_N) {
         *mi = 5;
         return n_out;
     }

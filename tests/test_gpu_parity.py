@@ -844,6 +844,33 @@ def test_gemm_wide_kernel(mi, n_out, n_in, n_tok, knobs):
     assert normwise(got["2"], O.gemm(W, Xq, n_out, n_in, n_tok, nthreads=16)) <= TOL
 
 
+@pytest.mark.parametrize("n_out,n_in,n_tok", [(17408, 5120, 768), (17408, 5120, 512), (6144, 5120, 2048),
+                                              (5120, 6144, 2048), (17408, 5120, 384)])
+def test_gemm_default_dispatch_single_round(n_out, n_in, n_tok, knobs):
+    """Shapes whose wide tiles fill less than one round of the CUs: the
+    default dispatch (one round of 256-row tiles at 17408x5120 M = 768 and
+    6144x5120 M = 2048, of 160-row tiles at 17408x5120 M = 512 and
+    5120x6144 M = 2048, the LDS kernel at M = 384) is bit-identical to the LDS
+    kernel alone and matches the oracle on a row sample."""
+    case(f"gemm default dispatch {n_out}x{n_in}x{n_tok}")
+    W = O.gen_weights(3600 + n_out + n_tok, n_out, n_in)
+    X = np.stack([O.fwht(O.gen_normal(3601 + t, n_in)) for t in range(n_tok)])
+    Xq = O.quantize_chunk_major(X)
+    Wd, Xd = dev(W), dev(Xq)
+    got = {}
+    for wide in ("1", "0"):
+        knobs.set("BONSAI_GEMM_WIDE", wide)
+        Y = torch.full((n_out, n_tok), float("nan"), dtype=torch.float32, device="cuda")
+        B.gemm(Wd, Xd, Y, n_out, n_in, n_tok)
+        got[wide] = host(Y)
+    assert np.all(np.isfinite(got["1"]))
+    np.testing.assert_array_equal(bits(got["1"]), bits(got["0"]))
+    rows = np.r_[0:48, n_out // 2 - 24:n_out // 2 + 24, n_out - 48:n_out]
+    rb = n_in // 128 * 34
+    Ws = np.concatenate([W[r * rb:(r + 1) * rb] for r in rows])
+    assert normwise(got["1"][rows], O.gemm(Ws, Xq, rows.size, n_in, n_tok, nthreads=16)) <= TOL
+
+
 @pytest.mark.parametrize("mi", ["8", "5"])
 def test_gemm_wide_kernel_edge_scales(mi, knobs):
     """The wide kernel on blocks with subnormal or zero scales and on blocks
