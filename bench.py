@@ -501,15 +501,17 @@ def mfma_peak(kind: int, iters: int = 4096, per_cu: int = 4):
     return tops, tops * 1e12 / ops_per_clk / 1e6
 
 
-def valu_mfma_overlap(iters: int = 4096, per_cu: int = 4):
-    """bonsai_p40_overlap_probe at 4 waves per SIMD: ms for 4 f16 MFMAs per
-    iteration alone, 16 fp32 FMAs alone (4 per MFMA: the prefill GEMM's
-    rescale ratio), and both in one wave stream."""
+def valu_mfma_overlap(iters: int = 4096, per_cu: int = 4,
+                      modes=(("mfma_only", 0), ("fma_only", 1), ("both", 2), ("gemm_core", 3))):
+    """bonsai_p40_overlap_probe at per_cu waves per SIMD (per_cu 4-wave
+    workgroups per CU): ms for 4 f16 MFMAs per iteration alone, 16 fp32 FMAs
+    alone (4 per MFMA: the prefill GEMM's rescale ratio), both in one wave
+    stream, and the GEMM's chunk step."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     blocks = per_cu * cus
     sink = torch.zeros(blocks, dtype=torch.int32, device="cuda")
     out = {}
-    for name, mode in (("mfma_only", 0), ("fma_only", 1), ("both", 2), ("gemm_core", 3)):
+    for name, mode in modes:
         B.overlap_probe(mode, 1, blocks, 64, sink)
         torch.cuda.synchronize()
         best = None
@@ -522,8 +524,9 @@ def valu_mfma_overlap(iters: int = 4096, per_cu: int = 4):
             ms = e0.elapsed_time(e1)
             best = ms if best is None else min(best, ms)
         out[name + "_us"] = round(best * 1e3, 2)
-    out["both_over_sum"] = round(out["both_us"] / (out["mfma_only_us"] + out["fma_only_us"]), 3)
-    out["both_over_max"] = round(out["both_us"] / max(out["mfma_only_us"], out["fma_only_us"]), 3)
+    if "both_us" in out:
+        out["both_over_sum"] = round(out["both_us"] / (out["mfma_only_us"] + out["fma_only_us"]), 3)
+        out["both_over_max"] = round(out["both_us"] / max(out["mfma_only_us"], out["fma_only_us"]), 3)
     # the GEMM's chunk step alone: iters steps per wave, 4 waves per SIMD, each
     # step a 32 x 32 x 32 piece of the product; scaled to the M = 2048
     # 17408x5120 prefill (5,570,560 such pieces over the CUs' SIMDs)
@@ -611,6 +614,10 @@ def main():
         for kind in (0, 1):
             print(f"[bench] mfma peak kind {kind}: {mfma_peak(kind)}", flush=True)
         print(f"[bench] valu/mfma overlap: {valu_mfma_overlap()}", flush=True)
+        for per_cu in (1, 2, 3, 4, 8):
+            core = valu_mfma_overlap(per_cu=per_cu, modes=(("gemm_core", 3),))
+            print(f"[bench] gemm core at {per_cu} waves per SIMD: "
+                  f"{core['gemm_core_floor_us_m2048_17408x5120']} us floor (17408x5120, M = 2048)", flush=True)
         print(f"[bench] dependent launch floor: {launch_floor():.3f} us", flush=True)
         return
     if args.only_read:
