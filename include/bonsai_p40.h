@@ -233,14 +233,16 @@ int bonsai_p40_rmsnorm_fwht_gemv_group(const void * const * W, float * const * y
 // (signs may be NULL); hq has n_ff/32 Q8_1 blocks.
 // workspace: BONSAI_P40_FFN_WORKSPACE_BYTES(n_ff) device bytes, 16-byte
 // aligned, ZERO-FILLED before its first use.  Its first
-// BONSAI_P40_FFN_SYNC_BYTES hold the launch's completion counters, which a
-// completed call leaves ready for the next one (do not modify them between
-// calls); the gate and up rows (fp32) follow.  Calls that may run at the
-// same time need their own workspaces.  status (device, may be NULL): the
-// kernel adds 1 for each internal wait that gave up (it then leaves hq partly
-// unwritten and the workspace must be zero-filled again).  Errors: 1 if a
-// pointer is NULL or misaligned, n_ff or n_embd <= 0 or not a multiple of
-// 1024.
+// BONSAI_P40_FFN_SYNC_BYTES are flags, then 2 n_ff words through which the
+// gate and up rows pass from the workgroups that compute them to the one that
+// finishes their 1024-block; a completed call leaves all of it zero again
+// (do not modify it between calls).  Calls that may run at the same time
+// need their own workspaces.  status (device, may be NULL): the kernel adds 1
+// for each internal wait that gave up (it then leaves hq partly unwritten and
+// the workspace must be zero-filled again).  On widths without the one-launch
+// kernel the call runs the grouped GEMV and the glue as two launches and the
+// rows stay in the workspace as plain fp32.  Errors: 1 if a pointer is NULL
+// or misaligned, n_ff or n_embd <= 0 or not a multiple of 1024.
 #define BONSAI_P40_FFN_SYNC_BYTES 256
 #define BONSAI_P40_FFN_WORKSPACE_BYTES(n_ff) (BONSAI_P40_FFN_SYNC_BYTES + 8 * (int64_t)(n_ff))
 int bonsai_p40_ffn_gate_up_swiglu(const void * Wg, const void * Wu, const float * x, const float * norm_w,
@@ -254,7 +256,8 @@ int bonsai_p40_ffn_gate_up_swiglu(const void * Wg, const void * Wu, const float 
 // reference.  The workspace is a static device array inside the library of
 // BONSAI_P40_FFN_WORKSPACE_BYTES(BONSAI_P40_FFN_NOALLOC_MAX_NFF) bytes (~512
 // KiB), one per GPU for the life of the process; the call allocates nothing
-// (two kernel launches: a counter clear, then the fused launch).  Every call
+// (two kernel launches: a check that repairs the array after a wait that gave
+// up, then the fused launch).  Every call
 // on one GPU shares that array, so calls that overlap on one GPU (different
 // streams, different host threads) race and must not be issued.  Errors: as
 // bonsai_p40_ffn_gate_up_swiglu, plus 1 if n_ff > BONSAI_P40_FFN_NOALLOC_MAX_NFF;

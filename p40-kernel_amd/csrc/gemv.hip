@@ -200,12 +200,16 @@ typedef int v4i_a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 
 
-// FFN epilogue of the gate/up group (EPI kernels only): once every workgroup
-// has stored its gate (y[0]) and up (y[1]) rows, hq = Q8_1(FWHT(h_signs .*
-// swiglu(gate, up))) per 1024-block.  sync[0] counts workgroups that stored
-// their rows (zero before a launch and again after it), sync[1] is a
-// generation number advanced once per launch.  status (may be null) counts
-// waits that gave up.
+// FFN epilogue of the gate/up group (EPI kernels only): hq = Q8_1(FWHT(h_signs
+// .* swiglu(gate, up))) per 1024-block, each block as soon as its 1024 gate
+// (y[0]) and 1024 up (y[1]) rows are stored.  The rows travel as the bitwise
+// complement of their fp32 bits, so that a zero word means "not written in
+// this launch" (no fp32 result of the GEMV has all bits set: a NaN it
+// produces is quiet with a payload from an input or the default one); the
+// block's finaliser clears them back to zero after reading them.  sync[1] is
+// set to 1 when a finaliser gave up (the rows are then not all cleared and
+// the workspace must be zero-filled again).  status (may be null) counts waits
+// that gave up.
 struct FfnEpilogue {
     uint32_t * sync;
     const float * h_signs;
@@ -256,98 +260,63 @@ __device__ __forceinline__ double * rms_partials() {
     return buf;
 }
 
-// Polls of the FFN epilogue's wait before it gives up (each poll is one
-// device-coherent load plus a short sleep: some tens of milliseconds in all).
+// Polls of an FFN block's wait before it gives up (each poll is 32
+// device-coherent loads per lane plus a short sleep: some tens of
+// milliseconds in all).
 constexpr uint32_t EPI_SPIN_LIMIT = 1u << 16;
 
-// FFN epilogue of the gate/up group kernel (src/ops.h:27-31 after the two
-// GEMVs).  Every workgroup read the generation word sync[1] when it started
-// (gen0: nothing advances it before every workgroup has taken its ticket),
-// stored its gate and up rows with device-coherent stores, waits for their
-// acknowledgement and takes one ticket from sync[0] with an agent-scope
-// acquire-release read-modify-write (the tickets form one release sequence).
-// The workgroup holding the last ticket has thereby acquired every row of
-// both matrices; it zeroes sync[0] and then advances sync[1] with a release
-// store, which the finalisers acquire.  The workgroups holding the last
-// nfin = min(#workgroups, nblk) tickets are the finalisers: each waits
-// (bounded) for sync[1] to move past the value it read (the last one does
-// not wait), then finishes the 1024-blocks f, f + nfin, ...: SwiGLU of the
-// block over all its threads into LDS (device-coherent loads), then one wave
-// applies the signs, rotates (fwht1024_regs) and quantises
-// (quant_pair_store) -- the device code of bonsai_p40_swiglu_fwht_quant, so
-// hq is the same bytes.  A finaliser whose wait gives up adds 1 to *status
-// and leaves its blocks unwritten.  Non-finalising workgroups leave right
-// after their ticket, which frees their CUs for any workgroup not yet
-// started, so the wait always ends.
-template <int WAVES>
-__device__ __forceinline__ void ffn_epilogue(const MatGroup & mg, float * h_lds, uint32_t gen0) {
+// One FFN block's glue by one wave: wait until the block's 1024 gate and 1024
+// up rows are all written (lane l polls the 16 gate and 16 up rows of its
+// FWHT row, a bounded poll of device-coherent loads), then SwiGLU, signs,
+// FWHT and Q8_1 in registers, and clear the rows for the next launch.  The
+// rows are single 32-bit atomic words, so a non-zero word read here is the
+// writer's store itself and no further ordering is needed.
+__device__ __forceinline__ void ffn_finalise_block(const MatGroup & mg, int b) {
     const FfnEpilogue & e = mg.epi;
-    __shared__ uint32_t epi_ticket, epi_gave_up;
-    wait_vmcnt<0>();                                   // this wave's rows are acknowledged
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __syncthreads();
-    const uint32_t nwg = gridDim.x;
-    const uint32_t nfin = nwg < (uint32_t)e.nblk ? nwg : (uint32_t)e.nblk;
-    if (threadIdx.x == 0) {
-        // release: this workgroup's rows (every wave's stores acknowledged
-        // above) before its ticket; acquire: the rows of every earlier ticket
-        const uint32_t t = __hip_atomic_fetch_add(&e.sync[0], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        uint32_t give = 0;
-        if (t == nwg - 1) {
-            // every workgroup's rows are acknowledged: reset the ticket counter
-            // for the next launch (nothing reads it again in this one) and open
-            // the finalisers' wait
-            __hip_atomic_store(&e.sync[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&e.sync[1], gen0 + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-        } else if (t >= nwg - nfin) {
-            uint32_t polls = 0;
-            while (__hip_atomic_load(&e.sync[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen0) {
-                if (++polls > EPI_SPIN_LIMIT) {
-                    give = 1;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            }
-            // pairs with the last ticket holder's release store
-            if (!give) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const int lane = threadIdx.x & 63;
+    const int row = fwht_row(lane);
+    uint32_t * g = reinterpret_cast<uint32_t *>(mg.y[0]) + (size_t)HBLK * b + 16 * row;
+    uint32_t * u = reinterpret_cast<uint32_t *>(mg.y[1]) + (size_t)HBLK * b + 16 * row;
+    uint32_t gv[16], uv[16];
+    uint32_t polls = 0;
+    bool ok = false;
+    for (;;) {
+        bool have = true;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            gv[r] = __hip_atomic_load(g + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            uv[r] = __hip_atomic_load(u + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            have = have && gv[r] != 0u && uv[r] != 0u;
         }
-        epi_ticket = t;
-        epi_gave_up = give;
+        if (__builtin_amdgcn_ballot_w64(!have) == 0) {
+            ok = true;
+            break;
+        }
+        if (++polls > EPI_SPIN_LIMIT) break;
+        __builtin_amdgcn_s_sleep(1);
     }
-    __syncthreads();
-    const uint32_t t = epi_ticket;
-    if (t < nwg - nfin) return;
-    if (epi_gave_up) {
-        if (threadIdx.x == 0 && e.status != nullptr)
-            __hip_atomic_fetch_add(e.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!ok) {
+        if (lane == 0) {
+            if (e.status != nullptr) __hip_atomic_fetch_add(e.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&e.sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         return;
     }
-    // every wave of a finaliser reads the rows after thread 0's acquire (the
-    // workgroup barrier above orders it)
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    for (int b = (int)(t - (nwg - nfin)); b < e.nblk; b += (int)nfin) {
-        const float * g = mg.y[0] + (size_t)HBLK * b;
-        const float * u = mg.y[1] + (size_t)HBLK * b;
-        for (int i = threadIdx.x; i < HBLK; i += 64 * WAVES) {
-            const float gv = __hip_atomic_load(g + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const float uv = __hip_atomic_load(u + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            h_lds[i] = swiglu1(gv, uv);
-        }
-        __syncthreads();
-        if (threadIdx.x < 64) {
-            const int l = threadIdx.x, row = fwht_row(l);
-            float v[16];
+    float v[16];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) v[r] = h_lds[16 * row + r];
-            if (e.h_signs != nullptr) {
-                const float * sg = e.h_signs + (size_t)HBLK * b + 16 * row;
+    for (int r = 0; r < 16; ++r) v[r] = swiglu1(__uint_as_float(~gv[r]), __uint_as_float(~uv[r]));
+    if (e.h_signs != nullptr) {
+        const float * sg = e.h_signs + (size_t)HBLK * b + 16 * row;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) v[r] *= sg[r];
-            }
-            fwht1024_regs(v, l);
-            quant_pair_store(v, e.hq + ((size_t)b * (HBLK / QK8) + (row >> 1)) * Q81_BYTES, row & 1);
-        }
-        __syncthreads();
+        for (int r = 0; r < 16; ++r) v[r] *= sg[r];
+    }
+    fwht1024_regs(v, lane);
+    quant_pair_store(v, e.hq + ((size_t)b * (HBLK / QK8) + (row >> 1)) * Q81_BYTES, row & 1);
+    // (the loads above are complete: their values were used)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        __hip_atomic_store(g + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(u + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -447,12 +416,23 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
     // one-wave-per-unit schedule, and no wave carries a whole extra unit.
     const int T = nb_tail_ok<NB, NT, RP, DUMP, EPI>() ? tail : 0;
     if (T > 0 && wave < T) --nu;
-    // EPI: the launch's generation, read at the start (its latency hides
-    // behind the first loads; only thread 0 of the workgroup uses it)
-    uint32_t epi_gen0 = 0;
-    if constexpr (EPI) {
-        if (threadIdx.x == 0) epi_gen0 = __hip_atomic_load(&mg.epi.sync[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    // EPI: the gate and up units of each 1024-row block are consecutive in the
+    // unit space (block k: 1024 / G gate units, then 1024 / G up units), so a
+    // block's rows are all computed within about one round of the grid and
+    // its glue can start while the stream continues
+    auto unit_at = [&](int uu, const uint8_t *& Wm, float *& ym, int & n_out_m, int & lu) {
+        if constexpr (EPI) {
+            constexpr int UPB = HBLK / P::G;                 // units per block per matrix
+            const int k = uu / (2 * UPB), r = uu - k * 2 * UPB;
+            const bool up = r >= UPB;
+            lu = k * UPB + (up ? r - UPB : r);
+            Wm = up ? mg.W[1] : mg.W[0];
+            ym = up ? mg.y[1] : mg.y[0];
+            n_out_m = mg.n_out[0];
+        } else {
+            gs.at(uu, Wm, ym, n_out_m, lu);
+        }
+    };
 
     // OVL: the fp32 blocks are staged in the unit ring itself (the widest rows,
     // where a separate stage does not fit beside an 8-wave ring): slots k =
@@ -531,7 +511,7 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         const uint8_t * Wm;
         float * ym;
         int n_out_m, lu;
-        gs.at(uu, Wm, ym, n_out_m, lu);
+        unit_at(uu, Wm, ym, n_out_m, lu);
         const uint64_t m_bytes = (uint64_t)n_out_m * (PQ2_BYTES * NB);
         if (m_bytes < 0x80000000ull) {
             // buffer DMA with the matrix as the range: the unit offset is one
@@ -747,6 +727,22 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         __builtin_amdgcn_wave_barrier();
     }
 
+    // EPI: a unit's rows are stored one step later, right after the next
+    // unit's wait, so that the store has a whole step to complete before a
+    // wait counts it (a store is a vmcnt event like the unit DMAs); the words
+    // are the complement of the fp32 bits, device-coherent
+    float pend0 = 0.0f, pend1 = 0.0f;
+    auto store_rows = [&](int uu, float r0, float r1) {
+        const uint8_t * Wm;
+        float * ym;
+        int n_out_m, lu;
+        unit_at(uu, Wm, ym, n_out_m, lu);
+        const int row = lu * P::G + lane;
+        if (lane < P::G && row < n_out_m)
+            __hip_atomic_store(reinterpret_cast<uint32_t *>(ym) + row, ~__float_as_uint(lane == 0 ? r0 : r1),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+
     int i = 0;
     if (nu > 0) do {
         const int slot = i % SL;
@@ -755,6 +751,9 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         else if (newer == 1) wait_vmcnt<P::NPL>();
         else wait_vmcnt<0>();
         __builtin_amdgcn_wave_barrier();
+        if constexpr (EPI) {
+            if (i > 0) store_rows(gw + (i - 1) * NW, pend0, pend1);
+        }
         // unit i + D goes into the slot unit i - 1 used (its reads completed:
         // lgkmcnt(0) at the end of the previous step)
         if (i + D < nu) issue(gw + (i + D) * NW, (i + D) % SL);
@@ -805,10 +804,16 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
                     const float v = wave_sum2_to_lanes31_63(acc0[t], acc1[t]);
                     const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
                     const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-                    ykeep = (lane == 2 * i * NT + t) ? t0 : ((lane == (2 * i + 1) * NT + t) ? t1 : ykeep);
+                    if constexpr (EPI) {
+                        pend0 = t0;
+                        pend1 = t1;
+                    } else {
+                        ykeep = (lane == 2 * i * NT + t) ? t0 : ((lane == (2 * i + 1) * NT + t) ? t1 : ykeep);
+                    }
                 } else {
                     const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_to_lane63(acc0[t])), 63));
-                    ykeep = (lane == i * NT + t) ? t0 : ykeep;
+                    if constexpr (EPI) pend0 = t0;
+                    else ykeep = (lane == i * NT + t) ? t0 : ykeep;
                 }
             }
         }
@@ -855,6 +860,13 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
             if (lane < P::G && row < n_out_m) ym[row] = lane == 0 ? t0 : t1;
         }
     }
+    if constexpr (EPI) {
+        if (nu > 0) store_rows(gw + (nu - 1) * NW, pend0, pend1);
+        // the last nblk waves of the numbering (those with the fewest units)
+        // each finalise the blocks b = NW - 1 - gw, + NW, ...
+        for (int b = NW - 1 - gw; b >= 0 && b < mg.epi.nblk; b += NW) ffn_finalise_block(mg, b);
+        return;
+    }
     if (!DUMP && lane < nu * P::G * NT) {
         const uint8_t * Wm;
         float * ym;
@@ -863,17 +875,11 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         gs.at(gw + (rt / P::G) * NW, Wm, ym, n_out_m, lu);
         const int row = lu * P::G + rt % P::G;
         if (NT == 1) {
-            // EPI: other workgroups read these rows in this launch, so the
-            // store is coherent at device scope (written through to memory)
-            if (row < n_out_m) {
-                if constexpr (EPI) __hip_atomic_store(ym + row, ykeep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                else ym[row] = ykeep;
-            }
+            if (row < n_out_m) ym[row] = ykeep;
         } else if (row < n_out_m && t < n_tok) {
             ym[(size_t)row * n_tok + t] = ykeep;
         }
     }
-    if constexpr (EPI) ffn_epilogue<WAVES>(mg, reinterpret_cast<float *>(&ring_all[0][0][0]), epi_gen0);
 }
 
 // Generic path: one wave per row, lane-strided chunks, 2-byte weight loads
@@ -1750,10 +1756,15 @@ constexpr size_t FFN_SCRATCH_BYTES = (size_t)BONSAI_P40_FFN_WORKSPACE_BYTES(FFN_
 
 __device__ __attribute__((aligned(256))) uint8_t scratch[FFN_SCRATCH_BYTES];
 
-// zeroes the ticket counter (the generation word may hold any value): a
-// kernel rather than a memset, so that a captured graph replays it correctly
-__global__ void __launch_bounds__(64) ffn_sync_clear_kernel(uint32_t * sync) {
-    if (threadIdx.x == 0) sync[0] = 0u;
+// Repair of the static workspace after a launch whose block wait gave up
+// (sync[1] set): zeroes the row words and the flag; otherwise it reads one
+// word and returns.  A kernel rather than a memset, so that a captured graph
+// replays it correctly.
+__global__ void __launch_bounds__(256) ffn_sync_clear_kernel(uint32_t * sync, uint32_t * rows, int n_words) {
+    if (__hip_atomic_load(&sync[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) return;
+    for (int i = threadIdx.x; i < n_words; i += 256) rows[i] = 0u;
+    __syncthreads();
+    if (threadIdx.x == 0) sync[1] = 0u;
 }
 
 struct ScratchAddr {
@@ -1879,7 +1890,8 @@ int bonsai_p40_ffn_gate_up_swiglu_noalloc(const void * Wg, const void * Wu, cons
     if (a.err != hipSuccess) return (int)a.err;
     hipStream_t st = (hipStream_t)stream;
     uint32_t * sync = reinterpret_cast<uint32_t *>(a.ptr);
-    hipLaunchKernelGGL(ffn_sync_clear_kernel, dim3(1), dim3(64), 0, st, sync);
+    hipLaunchKernelGGL(ffn_sync_clear_kernel, dim3(1), dim3(256), 0, st, sync,
+                       reinterpret_cast<uint32_t *>(a.ptr + BONSAI_P40_FFN_SYNC_BYTES), (int)(2 * n_ff));
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
     return pq2::ffn_gate_up_swiglu(Wg, Wu, x, norm_w, x_signs, h_signs, hq, n_ff, n_embd, eps, sync,
