@@ -266,27 +266,33 @@ __device__ __forceinline__ double * rms_partials() {
 constexpr uint32_t EPI_SPIN_LIMIT = 1u << 16;
 
 // One FFN block's glue by one wave: wait until the block's 1024 gate and 1024
-// up rows are all written (lane l polls the 16 gate and 16 up rows of its
-// FWHT row, a bounded poll of device-coherent loads), then SwiGLU, signs,
-// FWHT and Q8_1 in registers, and clear the rows for the next launch.  The
-// rows are single 32-bit atomic words, so a non-zero word read here is the
-// writer's store itself and no further ordering is needed.
-__device__ __forceinline__ void ffn_finalise_block(const MatGroup & mg, int b) {
+// up rows are all written (a bounded poll of device-coherent loads), then
+// SwiGLU, signs, FWHT and Q8_1 in registers, and clear the rows for the next
+// launch.  The rows are single 32-bit atomic words, so a non-zero word read
+// here is the writer's store itself and no further ordering is needed.  With
+// `stage` (8 KiB of this wave's own LDS) the words are polled coalesced (lane
+// l reads words 64 k + l) and reach the FWHT layout (lane l: the 16
+// consecutive rows of its FWHT row) through LDS; without it each lane polls
+// its 16 gate and 16 up rows directly.
+__device__ __forceinline__ void ffn_finalise_block(const MatGroup & mg, int b, float * stage) {
     const FfnEpilogue & e = mg.epi;
     const int lane = threadIdx.x & 63;
     const int row = fwht_row(lane);
-    uint32_t * g = reinterpret_cast<uint32_t *>(mg.y[0]) + (size_t)HBLK * b + 16 * row;
-    uint32_t * u = reinterpret_cast<uint32_t *>(mg.y[1]) + (size_t)HBLK * b + 16 * row;
+    uint32_t * g = reinterpret_cast<uint32_t *>(mg.y[0]) + (size_t)HBLK * b;
+    uint32_t * u = reinterpret_cast<uint32_t *>(mg.y[1]) + (size_t)HBLK * b;
+    // word k of this lane: index 64 k + lane (coalesced) or 16 row + k
+    const int base = stage != nullptr ? lane : 16 * row;
+    const int step = stage != nullptr ? 64 : 1;
     uint32_t gv[16], uv[16];
     uint32_t polls = 0;
     bool ok = false;
     for (;;) {
         bool have = true;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            gv[r] = __hip_atomic_load(g + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            uv[r] = __hip_atomic_load(u + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            have = have && gv[r] != 0u && uv[r] != 0u;
+        for (int k = 0; k < 16; ++k) {
+            gv[k] = __hip_atomic_load(g + base + step * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            uv[k] = __hip_atomic_load(u + base + step * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            have = have && gv[k] != 0u && uv[k] != 0u;
         }
         if (__builtin_amdgcn_ballot_w64(!have) == 0) {
             ok = true;
@@ -303,8 +309,20 @@ __device__ __forceinline__ void ffn_finalise_block(const MatGroup & mg, int b) {
         return;
     }
     float v[16];
+    if (stage != nullptr) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) v[r] = swiglu1(__uint_as_float(~gv[r]), __uint_as_float(~uv[r]));
+        for (int k = 0; k < 16; ++k) {
+            stage[64 * k + lane] = __uint_as_float(~gv[k]);
+            stage[HBLK + 64 * k + lane] = __uint_as_float(~uv[k]);
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);        // lgkmcnt(0): the stores are done
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v[r] = swiglu1(stage[16 * row + r], stage[HBLK + 16 * row + r]);
+    } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v[r] = swiglu1(__uint_as_float(~gv[r]), __uint_as_float(~uv[r]));
+    }
     if (e.h_signs != nullptr) {
         const float * sg = e.h_signs + (size_t)HBLK * b + 16 * row;
 #pragma unroll
@@ -314,9 +332,9 @@ __device__ __forceinline__ void ffn_finalise_block(const MatGroup & mg, int b) {
     quant_pair_store(v, e.hq + ((size_t)b * (HBLK / QK8) + (row >> 1)) * Q81_BYTES, row & 1);
     // (the loads above are complete: their values were used)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        __hip_atomic_store(g + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(u + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int k = 0; k < 16; ++k) {
+        __hip_atomic_store(g + base + step * k, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(u + base + step * k, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -416,23 +434,6 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
     // one-wave-per-unit schedule, and no wave carries a whole extra unit.
     const int T = nb_tail_ok<NB, NT, RP, DUMP, EPI>() ? tail : 0;
     if (T > 0 && wave < T) --nu;
-    // EPI: the gate and up units of each 1024-row block are consecutive in the
-    // unit space (block k: 1024 / G gate units, then 1024 / G up units), so a
-    // block's rows are all computed within about one round of the grid and
-    // its glue can start while the stream continues
-    auto unit_at = [&](int uu, const uint8_t *& Wm, float *& ym, int & n_out_m, int & lu) {
-        if constexpr (EPI) {
-            constexpr int UPB = HBLK / P::G;                 // units per block per matrix
-            const int k = uu / (2 * UPB), r = uu - k * 2 * UPB;
-            const bool up = r >= UPB;
-            lu = k * UPB + (up ? r - UPB : r);
-            Wm = up ? mg.W[1] : mg.W[0];
-            ym = up ? mg.y[1] : mg.y[0];
-            n_out_m = mg.n_out[0];
-        } else {
-            gs.at(uu, Wm, ym, n_out_m, lu);
-        }
-    };
 
     // OVL: the fp32 blocks are staged in the unit ring itself (the widest rows,
     // where a separate stage does not fit beside an 8-wave ring): slots k =
@@ -511,7 +512,7 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         const uint8_t * Wm;
         float * ym;
         int n_out_m, lu;
-        unit_at(uu, Wm, ym, n_out_m, lu);
+        gs.at(uu, Wm, ym, n_out_m, lu);
         const uint64_t m_bytes = (uint64_t)n_out_m * (PQ2_BYTES * NB);
         if (m_bytes < 0x80000000ull) {
             // buffer DMA with the matrix as the range: the unit offset is one
@@ -727,22 +728,6 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         __builtin_amdgcn_wave_barrier();
     }
 
-    // EPI: a unit's rows are stored one step later, right after the next
-    // unit's wait, so that the store has a whole step to complete before a
-    // wait counts it (a store is a vmcnt event like the unit DMAs); the words
-    // are the complement of the fp32 bits, device-coherent
-    float pend0 = 0.0f, pend1 = 0.0f;
-    auto store_rows = [&](int uu, float r0, float r1) {
-        const uint8_t * Wm;
-        float * ym;
-        int n_out_m, lu;
-        unit_at(uu, Wm, ym, n_out_m, lu);
-        const int row = lu * P::G + lane;
-        if (lane < P::G && row < n_out_m)
-            __hip_atomic_store(reinterpret_cast<uint32_t *>(ym) + row, ~__float_as_uint(lane == 0 ? r0 : r1),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    };
-
     int i = 0;
     if (nu > 0) do {
         const int slot = i % SL;
@@ -751,9 +736,6 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         else if (newer == 1) wait_vmcnt<P::NPL>();
         else wait_vmcnt<0>();
         __builtin_amdgcn_wave_barrier();
-        if constexpr (EPI) {
-            if (i > 0) store_rows(gw + (i - 1) * NW, pend0, pend1);
-        }
         // unit i + D goes into the slot unit i - 1 used (its reads completed:
         // lgkmcnt(0) at the end of the previous step)
         if (i + D < nu) issue(gw + (i + D) * NW, (i + D) % SL);
@@ -804,16 +786,10 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
                     const float v = wave_sum2_to_lanes31_63(acc0[t], acc1[t]);
                     const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
                     const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-                    if constexpr (EPI) {
-                        pend0 = t0;
-                        pend1 = t1;
-                    } else {
-                        ykeep = (lane == 2 * i * NT + t) ? t0 : ((lane == (2 * i + 1) * NT + t) ? t1 : ykeep);
-                    }
+                    ykeep = (lane == 2 * i * NT + t) ? t0 : ((lane == (2 * i + 1) * NT + t) ? t1 : ykeep);
                 } else {
                     const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_to_lane63(acc0[t])), 63));
-                    if constexpr (EPI) pend0 = t0;
-                    else ykeep = (lane == i * NT + t) ? t0 : ykeep;
+                    ykeep = (lane == i * NT + t) ? t0 : ykeep;
                 }
             }
         }
@@ -861,10 +837,25 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         }
     }
     if constexpr (EPI) {
-        if (nu > 0) store_rows(gw + (nu - 1) * NW, pend0, pend1);
+        // every row of the wave in one store: the complement of its fp32 bits as
+        // a device-coherent 32-bit atomic word (a finaliser polls for it)
+        if (lane < nu * P::G) {
+            const uint8_t * Wm;
+            float * ym;
+            int n_out_m, lu;
+            gs.at(gw + (lane / P::G) * NW, Wm, ym, n_out_m, lu);
+            const int row = lu * P::G + lane % P::G;
+            if (row < n_out_m)
+                __hip_atomic_store(reinterpret_cast<uint32_t *>(ym) + row, ~__float_as_uint(ykeep), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
         // the last nblk waves of the numbering (those with the fewest units)
         // each finalise the blocks b = NW - 1 - gw, + NW, ...
-        for (int b = NW - 1 - gw; b >= 0 && b < mg.epi.nblk; b += NW) ffn_finalise_block(mg, b);
+        // this wave's own ring (its units are done) stages the block when it is
+        // large enough: 8 KiB
+        float * stage = nullptr;
+        if constexpr (SL * P::LDSB >= 2 * HBLK * 4) stage = reinterpret_cast<float *>(&ring[0][0]);
+        for (int b = NW - 1 - gw; b >= 0 && b < mg.epi.nblk; b += NW) ffn_finalise_block(mg, b, stage);
         return;
     }
     if (!DUMP && lane < nu * P::G * NT) {
