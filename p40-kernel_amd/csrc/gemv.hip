@@ -338,6 +338,93 @@ __device__ __forceinline__ void ffn_finalise_block(const MatGroup & mg, int b, f
     }
 }
 
+// The finalising quad's LDS words: [0] quarters in LDS, [1] a quarter's
+// wait gave up.  Function-scope LDS, so only the FFN-epilogue kernels
+// allocate it.
+__device__ __forceinline__ uint32_t * ffn_quad_words() {
+    __shared__ uint32_t w[2];
+    return w;
+}
+
+// One FFN block's glue by four waves of one workgroup (quarter h = 0..3 of
+// the block, h = 3 also runs the rotation): each wave polls its quarter of
+// the block's gate and up words (lane l: words 256 h + 64 k + l, k < 4),
+// runs SwiGLU on them into its own LDS ring (1 KiB), clears the words and
+// counts itself in the workgroup's quad counter; the h = 3 wave waits
+// (bounded) for the four quarters, then reads the block in the FWHT layout
+// from the four rings, applies the signs, rotates and quantises.  quarter_lds
+// points at each wave's own 1 KiB; lds_of(q) at quarter q's.
+template <class F>
+__device__ __forceinline__ void ffn_finalise_quarter(const MatGroup & mg, int b, int h, float * quarter_lds,
+                                                     F lds_of) {
+    const FfnEpilogue & e = mg.epi;
+    const int lane = threadIdx.x & 63;
+    uint32_t * g = reinterpret_cast<uint32_t *>(mg.y[0]) + (size_t)HBLK * b + 256 * h + lane;
+    uint32_t * u = reinterpret_cast<uint32_t *>(mg.y[1]) + (size_t)HBLK * b + 256 * h + lane;
+    uint32_t * qw = ffn_quad_words();
+    uint32_t gv[4], uv[4];
+    uint32_t polls = 0;
+    bool ok = false;
+    for (;;) {
+        bool have = true;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            gv[k] = __hip_atomic_load(g + 64 * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            uv[k] = __hip_atomic_load(u + 64 * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            have = have && gv[k] != 0u && uv[k] != 0u;
+        }
+        if (__builtin_amdgcn_ballot_w64(!have) == 0) {
+            ok = true;
+            break;
+        }
+        if (++polls > EPI_SPIN_LIMIT) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (ok) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) quarter_lds[64 * k + lane] = swiglu1(__uint_as_float(~gv[k]), __uint_as_float(~uv[k]));
+        // (the loads above are complete: their values were used)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            __hip_atomic_store(g + 64 * k, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(u + 64 * k, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    } else if (lane == 0) {
+        if (e.status != nullptr) __hip_atomic_fetch_add(e.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&e.sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&qw[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    // publish the quarter to the rotating wave: its LDS stores, then the count
+    __builtin_amdgcn_s_waitcnt(0xC07F);            // lgkmcnt(0)
+    if (lane == 0) __hip_atomic_fetch_add(&qw[0], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (h != 3) return;
+    polls = 0;
+    while (__hip_atomic_load(&qw[0], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < 4u) {
+        if (++polls > EPI_SPIN_LIMIT) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (polls > EPI_SPIN_LIMIT || __hip_atomic_load(&qw[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u) {
+        if (polls > EPI_SPIN_LIMIT && lane == 0) {
+            if (e.status != nullptr) __hip_atomic_fetch_add(e.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&e.sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
+    const int row = fwht_row(lane);
+    // the FWHT row's 16 elements lie in quarter (16 row) / 256
+    const float * src = lds_of((16 * row) >> 8) + ((16 * row) & 255);
+    float v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[r] = src[r];
+    if (e.h_signs != nullptr) {
+        const float * sg = e.h_signs + (size_t)HBLK * b + 16 * row;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v[r] *= sg[r];
+    }
+    fwht1024_regs(v, lane);
+    quant_pair_store(v, e.hq + ((size_t)b * (HBLK / QK8) + (row >> 1)) * Q81_BYTES, row & 1);
+}
+
 // Workgroup of WAVES waves.  Each wave owns up to `units_per_wave` units
 // (grid-strided) and a private ring of D unit buffers in LDS; the workgroup shares one
 // LDS copy of the Q8_1 activation.  Every weight read is an LDS DMA
@@ -434,6 +521,17 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
     // one-wave-per-unit schedule, and no wave carries a whole extra unit.
     const int T = nb_tail_ok<NB, NT, RP, DUMP, EPI>() ? tail : 0;
     if (T > 0 && wave < T) --nu;
+    // EPI: tail != 0 means the launch's last round of units falls on waves
+    // below WAVES / 2 of every workgroup, so waves WAVES / 2 .. WAVES - 1 have
+    // the fewest units: those of workgroups 0 .. nblk - 1 finalise block
+    // blockIdx.x as a quad
+    const bool epi_quad = EPI && WAVES == 8 && tail != 0 && (int)blockIdx.x < mg.epi.nblk;
+    if constexpr (EPI) {
+        if (epi_quad && threadIdx.x == 0) {
+            ffn_quad_words()[0] = 0u;
+            ffn_quad_words()[1] = 0u;
+        }
+    }
 
     // OVL: the fp32 blocks are staged in the unit ring itself (the widest rows,
     // where a separate stage does not fit beside an 8-wave ring): slots k =
@@ -849,6 +947,15 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
                 __hip_atomic_store(reinterpret_cast<uint32_t *>(ym) + row, ~__float_as_uint(ykeep), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
         }
+        if (tail != 0) {
+            if (epi_quad && wave >= WAVES / 2) {
+                float * mine = reinterpret_cast<float *>(&ring[0][0]);
+                ffn_finalise_quarter(mg, (int)blockIdx.x, wave - WAVES / 2, mine, [&](int q) {
+                    return reinterpret_cast<const float *>(&ring_all[WAVES / 2 + q][0][0]);
+                });
+            }
+            return;
+        }
         // the last nblk waves of the numbering (those with the fewest units)
         // each finalise the blocks b = NW - 1 - gw, + NW, ...
         // this wave's own ring (its units are done) stages the block when it is
@@ -1017,6 +1124,20 @@ int launch_nb_t(MatGroup mg, int n_mat, const void * xin, const float * signs, i
     // numbering 2^xl must divide T * blocks / 8 (then unit index < L holds
     // exactly for waves < T) -- and every wave keeps D + 1 or more units
     int tail = 0;
+    if constexpr (EPI) {
+        // FFN epilogue: a four-wave quad per block (tail = 1) where waves
+        // WAVES / 2 .. WAVES - 1 of every workgroup carry the fewest units: the
+        // last round is complete, or is exactly the units of waves 0 .. T - 1,
+        // T <= WAVES / 2, of every workgroup (the numbering condition above)
+        const int nw = blocks * WAVES;
+        const int L = n_units - (upw - 1) * nw;
+        bool quad = WAVES == 8 && mg.epi.nblk <= blocks && knob(pq2host::K_FFN_QUAD, 1) != 0;
+        if (quad && L != nw) {
+            const int Tq = L / blocks;
+            quad = L % blocks == 0 && Tq <= WAVES / 2 && (xl == 0 || (Tq * (blocks / 8)) % (1 << xl) == 0);
+        }
+        tail = quad ? 1 : 0;
+    }
     if (nb_tail_ok<NB, NT, RP, DUMP, EPI>() && knob(pq2host::K_GEMV_TAIL, 0) != 0 && upw >= D + 1) {
         const int nw = blocks * WAVES;
         const int L = n_units - (upw - 1) * nw;

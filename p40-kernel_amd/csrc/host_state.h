@@ -46,6 +46,7 @@ enum Knob : int {
     K_GEMM_WIDE,
     K_GEMM_WIDE_MI,
     K_GEMV_TAIL,
+    K_FFN_QUAD,
     K_GGML_ENABLE,
     K_GGML_VERBOSE,
     K_COUNT
@@ -59,8 +60,8 @@ inline const char * knob_name(int k) {
         "BONSAI_GEMM_SMALL_GEMV",     "BONSAI_GEMM_BD",         "BONSAI_GEMM_SMALL",
         "BONSAI_GEMM_SMALL_CFG",      "BONSAI_GEMM_KERNEL",     "BONSAI_GEMM_F16_BN",
         "BONSAI_GEMM_F16_SPLIT",      "BONSAI_GEMM_F16_WAVES",  "BONSAI_GEMM_WIDE",
-        "BONSAI_GEMM_WIDE_MI",        "BONSAI_GEMV_TAIL",       "BONSAI_P40",
-        "BONSAI_P40_VERBOSE",
+        "BONSAI_GEMM_WIDE_MI",        "BONSAI_GEMV_TAIL",       "BONSAI_FFN_QUAD",
+        "BONSAI_P40",                 "BONSAI_P40_VERBOSE",
     };
     return names[k];
 }

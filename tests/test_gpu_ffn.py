@@ -105,6 +105,28 @@ def test_ffn_gate_up_swiglu_equals_separate_launches(n_ff, n_embd, rms, xsg, hsg
         assert int(host(status)[0]) == 0
 
 
+@pytest.mark.parametrize("n_ff,n_embd", [(17408, 5120), (5120, 6144), (1024, 5120), (3072, 1024)])
+def test_ffn_single_wave_finaliser(n_ff, n_embd, knobs):
+    """With the four-wave quads switched off (BONSAI_FFN_QUAD=0) each block is
+    finalised by one wave: the same bytes, the workspace back to zero."""
+    case(f"ffn_gate_up_swiglu single-wave finaliser n_ff={n_ff} n_embd={n_embd}")
+    knobs.set("BONSAI_FFN_QUAD", "0")
+    Wg = dev(O.gen_weights(6200 + n_ff, n_ff, n_embd))
+    Wu = dev(O.gen_weights(6201 + n_ff, n_ff, n_embd))
+    x = dev(O.gen_normal(6202 + n_embd, n_embd) * 2)
+    nw = dev(O.gen_normal(6203 + n_embd, n_embd) * 0.1 + 1)
+    hs = dev(signs(6204 + n_ff, n_ff))
+    ref_hq, _, _ = separate(Wg, Wu, x, nw, None, hs, n_ff, n_embd, 1e-6)
+    ws = torch.zeros(B.ffn_workspace_bytes(n_ff), dtype=torch.uint8, device="cuda")
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for rep in range(2):
+        hq = torch.full((B.q8_bytes(n_ff),), 0xAB, dtype=torch.uint8, device="cuda")
+        B.ffn_gate_up_swiglu(Wg, Wu, x, nw, None, hs, hq, n_ff, n_embd, 1e-6, ws, status)
+        np.testing.assert_array_equal(host(hq), ref_hq)
+        assert not np.any(host(ws).view(np.uint32))
+        assert int(host(status)[0]) == 0
+
+
 def test_ffn_gate_up_swiglu_against_oracle_chain():
     """Config 1 through the fused launch and the down GEMV, stage-wise against
     the oracle: gate/up (from the separate grouped launch, whose hq the fused
