@@ -141,9 +141,11 @@ def copies_for(nbytes: int, target: float = 1.1e9) -> int:
     return max(2, math.ceil(target / nbytes))
 
 
-def bench_gemv(n_out, n_in, steps, warmup, gen, n_tok=1, copies=0):
+def bench_gemv(n_out, n_in, steps, warmup, gen, n_tok=1, copies=0, ws=False):
     """us per launch over `copies` weight copies (0: enough to leave every
-    cache cold; 1: one copy reused, cache-warm)."""
+    cache cold; 1: one copy reused, cache-warm).  ws: the GEMM with its
+    workspace (bonsai_p40_gemm_ws; the workspace's conversion pass is inside
+    every timed call)."""
     W0 = synth_weights(n_out, n_in, gen)
     R = copies or copies_for(W0.numel())
     Ws = [W0] + [W0.clone() for _ in range(R - 1)]
@@ -151,6 +153,9 @@ def bench_gemv(n_out, n_in, steps, warmup, gen, n_tok=1, copies=0):
     y = torch.empty(n_out * n_tok, dtype=torch.float32, device="cuda")
     if n_tok == 1:
         fn = lambda i: B.gemv(Ws[i % R], xq, y, n_out, n_in)  # noqa: E731
+    elif ws:
+        wsb = torch.empty(max(16, B.gemm_workspace_bytes(n_in, n_tok)), dtype=torch.uint8, device="cuda")
+        fn = lambda i: B.gemm_ws(Ws[i % R], xq, y, n_out, n_in, n_tok, wsb)  # noqa: E731
     else:
         fn = lambda i: B.gemm(Ws[i % R], xq, y, n_out, n_in, n_tok)  # noqa: E731
     ms = time_loop(fn, steps, warmup)
@@ -602,6 +607,7 @@ def main():
                     help="stream-read probe over 23,750,272-byte buffers only (PMC calibration)")
     ap.add_argument("--shape", default=f"{N_FF}x{N_EMBD}", metavar="ROWSxCOLS",
                     help="matrix of --only-gemm / --only-small (default the headline 17408x5120)")
+    ap.add_argument("--ws", action="store_true", help="--only-gemm through bonsai_p40_gemm_ws")
     ap.add_argument("--only-gemm", type=int, default=0, metavar="M",
                     help="prefill GEMM 17408x5120 with M tokens only (profiling)")
     ap.add_argument("--only-small", type=int, default=0, metavar="B",
@@ -649,7 +655,7 @@ def main():
     if args.only_gemm or args.only_small:
         m = args.only_gemm or args.only_small
         no, ni = map(int, args.shape.split("x"))
-        ms = bench_gemv(no, ni, args.steps, args.warmup, gen, n_tok=m)
+        ms = bench_gemv(no, ni, args.steps, args.warmup, gen, n_tok=m, ws=args.ws)
         if args.only_gemm:
             tops = 2.0 * m * no * ni / (ms * 1e-3) / 1e12
             print(f"[bench] gemm {no}x{ni} M={m}: {ms * 1e3:.1f} us  {tops:.1f} TOPS", file=sys.stderr, flush=True)
@@ -801,12 +807,16 @@ def main():
         print(f"[bench] small batch done", file=sys.stderr, flush=True)
         for M in (512, 2048):
             for (n_out, n_in) in ((N_FF, N_EMBD), (N_EMBD, N_FF)):
-                m = bench_gemv(n_out, n_in, 10, 3, gen, n_tok=M)
+                m = bench_gemv(n_out, n_in, 10, 3, gen, n_tok=M, ws=True)
+                m0 = bench_gemv(n_out, n_in, 10, 3, gen, n_tok=M)
                 tops = 2.0 * M * n_out * n_in / (m * 1e-3) / 1e12
                 extra[f"prefill_M{M}_{n_out}x{n_in}"] = {
                     "us": round(m * 1e3, 1), "TOPS": round(tops, 1),
                     "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
-                    "frac_int8_probe": round(tops / peaks["int8"]["TOPS"], 4)}
+                    "frac_int8_probe": round(tops / peaks["int8"]["TOPS"], 4),
+                    "us_without_workspace": round(m0 * 1e3, 1),
+                    "note": "bonsai_p40_gemm_ws (its activation conversion pass included); "
+                            "us_without_workspace: bonsai_p40_gemm, the reference's signature"}
                 print(f"[bench] prefill M={M} {n_out}x{n_in}: {extra[f'prefill_M{M}_{n_out}x{n_in}']}",
                       file=sys.stderr, flush=True)
 

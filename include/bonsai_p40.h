@@ -76,6 +76,26 @@ int bonsai_p40_quant_activations(const float * x, void * out, int64_t n, bonsai_
 int bonsai_p40_gemm(const void * W, const void * Xq, float * Y,
                     int64_t n_out, int64_t n_in, int64_t n_tok, bonsai_stream stream);
 
+// bonsai_p40_gemm with a caller workspace (an addition; the reference has no
+// counterpart): where the long-prompt kernel runs (the rows bonsai_p40_gemm
+// gives its 256- or 160-row tiles) on a matrix of 8192 rows or more, Xq is
+// first converted once into the workspace (each q byte as f16, each d as
+// fp32: both exact), and the tiles take the activation from there by DMA
+// instead of converting it per tile; elsewhere it runs bonsai_p40_gemm.
+// Y is bit-identical to bonsai_p40_gemm's.  workspace: 16-byte aligned,
+// bonsai_p40_gemm_workspace_bytes(n_in, n_tok) bytes; NULL (any ws_bytes)
+// runs bonsai_p40_gemm.  The workspace is scratch for the call (stream-
+// ordered: calls that share one must be ordered on one stream).  Errors: those
+// of bonsai_p40_gemm, and 1 if workspace is not 16-byte aligned or ws_bytes is
+// smaller than the size the call needs.
+int bonsai_p40_gemm_ws(const void * W, const void * Xq, float * Y, int64_t n_out, int64_t n_in,
+                       int64_t n_tok, void * workspace, int64_t ws_bytes, bonsai_stream stream);
+// Workspace bytes bonsai_p40_gemm_ws needs (n_tok * n_in / 32 * 68); 0 where
+// it needs none (n_in or n_tok <= 0, or the converted activation would not
+// be addressable with 32-bit offsets: 2 GiB and more, the call then runs
+// bonsai_p40_gemm whatever the workspace).
+int64_t bonsai_p40_gemm_workspace_bytes(int64_t n_in, int64_t n_tok);
+
 // --- aligned repacked layout ------------------------------------------------
 // Size-neutral row: d[nb] fp16, then 4 planes of nb 8-byte code units; unit
 // u = plane*nb + block at byte 2*nb + 8u (src/pq2_0_repack.h:46-57).

@@ -30,6 +30,8 @@ SIGNATURES = {
     "bonsai_p40_gemv": [_V, _V, _F32P, _I64, _I64, _V],
     "bonsai_p40_quant_activations": [_F32P, _V, _I64, _V],
     "bonsai_p40_gemm": [_V, _V, _F32P, _I64, _I64, _I64, _V],
+    "bonsai_p40_gemm_ws": [_V, _V, _F32P, _I64, _I64, _I64, _V, _I64, _V],
+    "bonsai_p40_gemm_workspace_bytes": [_I64, _I64],
     "bonsai_p40_repack": [_V, _V, _I64, _I64, _V],
     "bonsai_p40_gemv_repack": [_V, _F32P, _F32P, _I64, _I64, _V],
     "bonsai_p40_fwht": [_F32P, _F32P, _I64, _V],
@@ -64,7 +66,7 @@ SIGNATURES = {
     "bonsai_p40_chain_plan": [_V, C.c_int, _V],
     "bonsai_p40_chain_run": [_V, C.c_int, _V, _V, _V],
 }
-RESTYPES = {"bonsai_p40_chain_plan_bytes": C.c_int64}
+RESTYPES = {"bonsai_p40_chain_plan_bytes": C.c_int64, "bonsai_p40_gemm_workspace_bytes": C.c_int64}
 
 _lib = None
 
@@ -129,6 +131,20 @@ def quant_activations(x, out, n: int, stream=None) -> None:
 
 def gemm(W, Xq, Y, n_out: int, n_in: int, n_tok: int, stream=None) -> None:
     _check("bonsai_p40_gemm", call("bonsai_p40_gemm", W, Xq, Y, n_out, n_in, n_tok, stream=stream))
+
+
+def gemm_workspace_bytes(n_in: int, n_tok: int) -> int:
+    """bonsai_p40_gemm_workspace_bytes: the workspace bonsai_p40_gemm_ws needs."""
+    return int(lib().bonsai_p40_gemm_workspace_bytes(n_in, n_tok))
+
+
+def gemm_ws(W, Xq, Y, n_out: int, n_in: int, n_tok: int, ws, ws_bytes=None, stream=None) -> None:
+    """bonsai_p40_gemm with a workspace (a tensor, or a pointer with ws_bytes);
+    Y is bit-identical to gemm()'s."""
+    if ws_bytes is None:
+        ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    _check("bonsai_p40_gemm_ws", call("bonsai_p40_gemm_ws", W, Xq, Y, n_out, n_in, n_tok, ws, ws_bytes,
+                                      stream=stream))
 
 
 def repack(src, dst, n_out: int, n_in: int, stream=None) -> None:

@@ -1266,12 +1266,17 @@ int64_t gemm_wide_rows(const void * W, const void * Xq, int64_t n_out, int64_t n
                        int * mi);
 int gemm_wide_launch(const void * W, const void * Xq, float * Y, int64_t n_out, int64_t n_tok, int nb, int mi,
                      hipStream_t st);
+int64_t gemm_wide_x16_bytes(int64_t n_tok, int nb);
+int gemm_wide_launch_ws(const void * W, const void * Xq, float * Y, int64_t n_out, int64_t n_tok, int nb, int mi,
+                        void * ws, hipStream_t st);
 }
 
-extern "C" {
+namespace {
 
-int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, int64_t n_in,
-                    int64_t n_tok, bonsai_stream stream) {
+// bonsai_p40_gemm's dispatch; ws (non-NULL: large enough and aligned, checked
+// by the caller) lets the long-prompt kernel take the activation by DMA
+int gemm_dispatch(const void * W, const void * Xq, float * Y, int64_t n_out, int64_t n_in, int64_t n_tok,
+                  void * ws, bonsai_stream stream) {
     if (n_in <= 0 || n_in % QK_PQ2 != 0) return 1;
     if (n_out <= 0 || n_tok <= 0) return 0;
     if (((uintptr_t)Xq & 3u) != 0 || ((uintptr_t)W & 1u) != 0 || pq2host::any_null(W, Xq, Y)) return 1;
@@ -1334,7 +1339,14 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
             int mi = 8;
             const int64_t rows = pq2::gemm_wide_rows(W, Xq, n_out, n_tok, nb, gemm_cu_count(), wide == 2, &mi);
             if (rows > 0) {
-                const int rc = pq2::gemm_wide_launch(W, Xq, Y, rows, n_tok, nb, mi, st);
+                // with a workspace: the activation converted once (an extra
+                // pass of 100 B per Q8_1 block), then the tiles DMA it -- worth
+                // it where that pass is spread over enough rows (measured on
+                // MI355X, M = 2048: 17408x5120 425 -> 414 us, 5120x17408 450 ->
+                // 459 us, so 8192 rows and more)
+                const bool via_ws = ws != nullptr && n_out >= 8192;
+                const int rc = via_ws ? pq2::gemm_wide_launch_ws(W, Xq, Y, rows, n_tok, nb, mi, ws, st)
+                                      : pq2::gemm_wide_launch(W, Xq, Y, rows, n_tok, nb, mi, st);
                 if (rc != 0 || rows == n_out) return rc;
                 return gemm_prefill_f16(w + (size_t)rows * PQ2_BYTES * nb, x, Y + (size_t)rows * n_tok,
                                         n_out - rows, n_tok, nb, st);
@@ -1350,6 +1362,29 @@ int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, i
         launch_gemm<4, 2, 1, 2>(w, x, Y, (int)n_out, (int)n_tok, nb, st);
     }
     return (int)hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" {
+
+int bonsai_p40_gemm(const void * W, const void * Xq, float * Y, int64_t n_out, int64_t n_in,
+                    int64_t n_tok, bonsai_stream stream) {
+    return gemm_dispatch(W, Xq, Y, n_out, n_in, n_tok, nullptr, stream);
+}
+
+int64_t bonsai_p40_gemm_workspace_bytes(int64_t n_in, int64_t n_tok) {
+    if (n_in <= 0 || n_tok <= 0 || n_in % QK_PQ2 != 0 || n_in / QK_PQ2 > (1 << 24)) return 0;
+    return pq2::gemm_wide_x16_bytes(n_tok, (int)(n_in / QK_PQ2));
+}
+
+int bonsai_p40_gemm_ws(const void * W, const void * Xq, float * Y, int64_t n_out, int64_t n_in,
+                       int64_t n_tok, void * workspace, int64_t ws_bytes, bonsai_stream stream) {
+    if (workspace == nullptr) return gemm_dispatch(W, Xq, Y, n_out, n_in, n_tok, nullptr, stream);
+    if (((uintptr_t)workspace & 15u) != 0) return 1;
+    const int64_t need = bonsai_p40_gemm_workspace_bytes(n_in, n_tok);
+    if (ws_bytes < need) return 1;
+    return gemm_dispatch(W, Xq, Y, n_out, n_in, n_tok, need > 0 ? workspace : nullptr, stream);
 }
 
 }  // extern "C"

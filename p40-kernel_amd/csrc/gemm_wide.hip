@@ -56,6 +56,7 @@
 // Requirements (checked by gemm_wide_rows): nb even, W and Xq 4-byte aligned,
 // the matrix and Xq each below 2 GiB (buffer descriptors with 32-bit ranges).
 #include "pq2_device.h"
+#include "gemv_device.h"
 #include "host_state.h"
 #include "../../include/bonsai_p40.h"
 
@@ -76,7 +77,7 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 // (tokens), a wave owning MI x 4 MFMA tiles of 16 x 16 (MI = 8: 256 rows;
 // MI = 5: 160 rows, the tile that fills one round for 5120-row matrices).
 constexpr int WB_N = 256, W_NI = 4;
-template <int MI>
+template <int MI, bool BD = false>
 struct WideCfg {
     static constexpr int BM = 32 * MI;
     static constexpr int ST_A = BM * 64;          // one chunk of f16 A: [row][32 positions]
@@ -84,8 +85,13 @@ struct WideCfg {
     static constexpr int ST_D = WB_N * 4;         // one chunk of fp32 activation scales
     static constexpr int ST = ST_A + ST_B + ST_D; // bytes per LDS slot
     // 2 slots for 256-row tiles (4 would spill registers), 4 for 160-row ones
-    // (measured faster there: 5120x17408 at M = 2048 ~490 against ~510 us)
-    static constexpr int RING = MI == 8 ? 2 : 4;
+    // (measured faster there: 5120x17408 at M = 2048 ~490 against ~510 us);
+    // with the activation by DMA (BD) 2 A slots and a barrier after every
+    // chunk, the B tiles and scales in RB slots of their own
+    static constexpr int RING = (MI == 8 || BD) ? 2 : 4;
+    static constexpr int SA = BD ? ST_A : ST;     // bytes per ring slot
+    static constexpr int RB = 4;                  // BD: B slots (chunk c in slot c % 4)
+    static constexpr int SB = ST_B + ST_D;        // BD: bytes per B slot
 };
 
 // Byte offset of 16-byte group g of row r in a [rows][64 B] tile, XOR-swizzled
@@ -154,14 +160,61 @@ __device__ __forceinline__ uint32_t wide_load_dw(__amdgpu_buffer_rsrc_t rw, uint
     return __builtin_amdgcn_raw_buffer_load_b32(rw, row_off, EVEN ? w_soff : w_soff - 2, 0);
 }
 
-template <int MI>
+// BD: one chunk's f16 activation tile and fp32 scales by LDS-DMA into a B
+// slot, three instructions per wave: the wave's two 1 KB pieces of the
+// [token][64 B] tile (lane offsets b0, b1 carry the tile's group swizzle) and
+// the scales of its 32 tokens (4 bytes per lane, lanes 0..31); soff_b /
+// soff_d = the chunk's byte offset in X16 / XD.
+__device__ __forceinline__ void wide_b_dma(__amdgpu_buffer_rsrc_t rxh, __amdgpu_buffer_rsrc_t rxd, uint8_t * slot,
+                                           int wave, int lane, uint32_t b0, uint32_t b1, uint32_t dl, uint32_t soff_b,
+                                           uint32_t soff_d, int d_at) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rxh, (lds_void *)(slot + 2048 * wave), 16, b0, soff_b, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rxh, (lds_void *)(slot + 2048 * wave + 1024), 16, b1, soff_b, 0, 0);
+    if (lane < 32)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rxd, (lds_void *)(slot + d_at + 128 * wave), 4, dl, soff_d, 0, 0);
+}
+
+// BD: A-side buffer loads issued at the step that loads chunk position j (the
+// code window: 2 dwords for an even block, 1 for an odd one; the block scale
+// dword with the block's first chunk), and the explicit wait at the end of
+// step J for the B slot DMA'd two steps before: the wave's VMEM instructions
+// younger than it are steps J - 1 and J, each A loads then 3 DMAs
+constexpr int wide_na(int j) { return ((j & 7) < 4 ? 2 : 1) + ((j & 3) == 0 ? 1 : 0); }
+template <int J, int LOAD>
+constexpr int wide_bd_wait() { return wide_na(J - 1 + LOAD) + 3 + wide_na(J + LOAD) + 3; }
+
+// The activation in the layout the BD kernel DMAs: block b of the chunk-major
+// Q8_1 X (36 B at 36 b) becomes 64 B of f16 at X16 + 64 b (q byte e -> f16 e,
+// exact) and its d as fp32 at XD[b] (exact); two threads per block.
+__global__ void __launch_bounds__(256)
+wide_x16_kernel(const uint8_t * __restrict__ Xq, uint8_t * __restrict__ X16, float * __restrict__ XD, int64_t blocks) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t b = i >> 1;
+    const int h = (int)(i & 1);
+    if (b >= blocks) return;
+    const uint32_t * src = reinterpret_cast<const uint32_t *>(Xq + b * Q81_BYTES);
+    uint32_t o[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) q4_f16(src[1 + 4 * h + k], o[2 * k], o[2 * k + 1]);
+    v4u * dst = reinterpret_cast<v4u *>(X16 + b * 64 + 32 * h);
+    dst[0] = (v4u){o[0], o[1], o[2], o[3]};
+    dst[1] = (v4u){o[4], o[5], o[6], o[7]};
+    if (h == 0) XD[b] = f16_bits_to_f32(src[0] & 0xffffu);
+}
+
+template <int MI, bool BD>
 __global__ void __launch_bounds__(512)
 gemm_wide_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X, float * __restrict__ Y,
-                 int n_out, int n_tok, int nb) {
-    using C = WideCfg<MI>;
-    constexpr int WB_M = C::BM, ST_A = C::ST_A, ST_B = C::ST_B, ST = C::ST, RING = C::RING;
+                 int n_out, int n_tok, int nb, const uint8_t * __restrict__ X16, const float * __restrict__ XD) {
+    using C = WideCfg<MI, BD>;
+    constexpr int WB_M = C::BM, ST_A = C::ST_A, ST_B = C::ST_B, ST = C::ST, RING = C::RING, SA = C::SA;
     constexpr int LEAD = RING == 4 ? 3 : 2, LOAD = LEAD + 2;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[RING * ST];
+    static_assert(!BD || (RING == 2 && LOAD == 4), "BD: the B DMA runs 4 chunks ahead");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[RING * SA];
+    // BD: the B slots as separate LDS objects, so that reads of one slot are
+    // not ordered behind the DMA into another
+    __shared__ __attribute__((aligned(16))) uint8_t sb0[BD ? C::SB : 16], sb1[BD ? C::SB : 16],
+        sb2[BD ? C::SB : 16], sb3[BD ? C::SB : 16];
     __shared__ int sBig;
 
     const int tid = threadIdx.x;
@@ -187,11 +240,35 @@ gemm_wide_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(X), (short)0, (int)(x_chunk * (uint32_t)nc), 0x00020000);
     const int wa = wswz(sr, 2 * sh);                                     // group 2 sh; 2 sh + 1 at wa1
     const int wa1 = wswz(sr, 2 * sh + 1);
-    const int wd = ST_A + ST_B + 4 * sr;
+    const int wd = ST_B + 4 * sr;                                        // in the B slot
     // ---- fragment reads -------------------------------------------------------
     const int ra = wswz(wm * 16 * MI + l16, g);                          // + 1024 mi
-    const int rb = ST_A + wswz(wn * 64 + l16, g);                        // + 1024 ni
-    const int rd = ST_A + ST_B + 4 * (wn * 64 + l16);                    // + 64 ni
+    const int rb = wswz(wn * 64 + l16, g);                               // in the B slot, + 1024 ni
+    const int rd = ST_B + 4 * (wn * 64 + l16);                           // in the B slot, + 64 ni
+    // LDS slot bases: ring slot st of A; B slot s (tile, then scales)
+    auto a_slot = [&](int st) __attribute__((always_inline)) { return smem + st * SA; };
+    auto b_slot = [&](int s) __attribute__((always_inline)) -> uint8_t * {
+        if constexpr (BD) return s == 0 ? sb0 : (s == 1 ? sb1 : (s == 2 ? sb2 : sb3));
+        else return smem + s * ST + ST_A;
+    };
+    // ---- BD: the activation tile and scales by DMA from X16 / XD ---------------
+    // (tokens past n_tok re-read the last token, as the staged path does)
+    const uint32_t x16_chunk = (uint32_t)n_tok * 64u, xd_chunk = (uint32_t)n_tok * 4u;
+    __amdgpu_buffer_rsrc_t rxh = rx, rxd = rx;
+    uint32_t b_l0 = 0, b_l1 = 0, d_l = 0;
+    if constexpr (BD) {
+        rxh = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(X16), (short)0, (int)(x16_chunk * (uint32_t)nc),
+                                                0x00020000);
+        rxd = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(XD), (short)0, (int)(xd_chunk * (uint32_t)nc),
+                                                0x00020000);
+        auto bsrc = [&](int r) {
+            const int p = (lane & 3) ^ (((r >> 1) ^ (r >> 2)) & 3);      // logical group at physical lane & 3
+            return (uint32_t)min(tok0 + r, n_tok - 1) * 64u + 16u * (uint32_t)p;
+        };
+        b_l0 = bsrc(32 * wave + (lane >> 2));
+        b_l1 = bsrc(32 * wave + 16 + (lane >> 2));
+        d_l = (uint32_t)min(tok0 + 32 * wave + lane, n_tok - 1) * 4u;
+    }
 
     v4f acc[MI][W_NI];
 #pragma unroll
@@ -220,7 +297,7 @@ gemm_wide_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
             constexpr bool even = (j >> 2) == 0;
             const int cc = c < nc ? c : c - 8;                            // past the end: two blocks back (same alignment)
             const uint32_t w_soff = 34u * (uint32_t)(cc >> 2);
-            if (stage_a) {
+            if (BD || stage_a) {                                          // (BD: every wave, for exact counts)
                 wide_load_a<p, even>(rw, a_off, w_soff, r);
                 if constexpr (p == 0) rdw = wide_load_dw<even>(rw, a_row, w_soff);
             }
@@ -231,7 +308,24 @@ gemm_wide_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
         };
         auto load_chunk = [&](int c, auto jc, WideRaw & r) __attribute__((always_inline)) {
             load_chunk_a(c, jc, r);
-            load_chunk_b(c, r);
+            if constexpr (!BD) load_chunk_b(c, r);
+        };
+        // BD: chunk c's tile and scales into B slot c % 4
+        auto dma_chunk = [&](int c, int s) __attribute__((always_inline)) {
+            const int cc = c < nc ? c : c - 8;
+            wide_b_dma(rxh, rxd, b_slot(s), wave, lane, b_l0, b_l1, d_l, (uint32_t)cc * x16_chunk,
+                       (uint32_t)cc * xd_chunk, ST_B);
+        };
+        // end-of-step barrier: BD waits for LDS only (a full fence would also
+        // wait for the B DMAs still in flight), with a compiler memory barrier
+        auto step_barrier = [&]() __attribute__((always_inline)) {
+            if constexpr (BD) {
+                __builtin_amdgcn_s_waitcnt(0xC07F);                      // lgkmcnt(0)
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+            } else {
+                __syncthreads();
+            }
         };
         // block table from the loaded scale dword (odd: the block is odd, its
         // scale in the dword's high half)
@@ -257,18 +351,18 @@ gemm_wide_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
         uint32_t cw = 0;                                                  // the realigned code dword
         uint32_t plo = 0, phi = 0;                                        // the even piece, held for the write
         auto convert_piece = [&](const WideRaw & r, int k, bool even, int st) __attribute__((always_inline)) {
-            uint8_t * sbase = smem + st * ST;
             uint32_t lo, hi;
+            if (BD && k >= 4) return;                                     // BD: B arrives by DMA
             if (k < 4) {
                 if (!stage_a) return;
                 if (k == 0) cw = even ? __builtin_amdgcn_alignbyte(r.a1, r.a0, 2) : r.a0;
                 codes4_lookup((cw >> (2 * k)) & 0x03030303u, tl, th, lo, hi);
-                if (k & 1) *reinterpret_cast<v4u *>(sbase + ((k & 2) ? wa1 : wa)) = (v4u){plo, phi, lo, hi};
+                if (k & 1) *reinterpret_cast<v4u *>(a_slot(st) + ((k & 2) ? wa1 : wa)) = (v4u){plo, phi, lo, hi};
             } else {
                 const uint32_t q4 = k == 4 ? r.q.x : k == 5 ? r.q.y : k == 6 ? r.q.z : r.q.w;
                 q4_f16(q4, lo, hi);
-                if (k & 1) *reinterpret_cast<v4u *>(sbase + ST_A + ((k & 2) ? wa1 : wa)) = (v4u){plo, phi, lo, hi};
-                if (k == 7 && sh == 0) *reinterpret_cast<float *>(sbase + wd) = f16_bits_to_f32(r.d & 0xffffu);
+                if (k & 1) *reinterpret_cast<v4u *>(b_slot(st) + ((k & 2) ? wa1 : wa)) = (v4u){plo, phi, lo, hi};
+                if (k == 7 && sh == 0) *reinterpret_cast<float *>(b_slot(st) + wd) = f16_bits_to_f32(r.d & 0xffffu);
             }
             if (!(k & 1)) {
                 plo = lo;
@@ -284,30 +378,49 @@ gemm_wide_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
         v8h Bf[W_NI];
         float dv[W_NI];
         auto load_frag_a = [&](int st, int mi) __attribute__((always_inline)) {
-            A[mi] = *reinterpret_cast<const v8h *>(smem + st * ST + ra + 1024 * mi);
+            A[mi] = *reinterpret_cast<const v8h *>(a_slot(st) + ra + 1024 * mi);
         };
-        auto load_frag_b = [&](int st, int ni) __attribute__((always_inline)) {
-            Bf[ni] = *reinterpret_cast<const v8h *>(smem + st * ST + rb + 1024 * ni);
+        auto load_frag_b = [&](int s, int ni) __attribute__((always_inline)) {
+            Bf[ni] = *reinterpret_cast<const v8h *>(b_slot(s) + rb + 1024 * ni);
         };
-        auto load_scale = [&](int st, int ni) __attribute__((always_inline)) {
-            dv[ni] = *reinterpret_cast<const float *>(smem + st * ST + rd + 64 * ni);
+        auto load_scale = [&](int s, int ni) __attribute__((always_inline)) {
+            dv[ni] = *reinterpret_cast<const float *>(b_slot(s) + rd + 64 * ni);
         };
 
         // ---- prologue: chunks 0 .. LEAD-1 converted, LEAD and LEAD+1 in flight -
-        load_chunk(0, std::integral_constant<int, 0>{}, raw[0]);
-        load_chunk(1, std::integral_constant<int, 1>{}, raw[1]);
-        build_table(0);
-        convert(raw[0], 0, 0);
-        convert(raw[1], 1, 1);
-        load_chunk(2, std::integral_constant<int, 2>{}, raw[0]);
-        if constexpr (RING == 4) {
-            convert(raw[0], 2, 2);
-            load_chunk(3, std::integral_constant<int, 3>{}, raw[1]);
-            load_chunk(4, std::integral_constant<int, 4>{}, raw[0]);
+        if constexpr (BD) {
+            // every chunk's A loads, then its B DMA, in chunk order (the
+            // order the step waits count on): chunks 0..3 in flight, 0 and 1
+            // converted; chunk 1's B (and so chunk 0's) has landed before the
+            // barrier
+            load_chunk_a(0, std::integral_constant<int, 0>{}, raw[0]);
+            dma_chunk(0, 0);
+            load_chunk_a(1, std::integral_constant<int, 1>{}, raw[1]);
+            dma_chunk(1, 1);
+            build_table(0);
+            convert(raw[0], 0, 0);
+            convert(raw[1], 1, 1);
+            load_chunk_a(2, std::integral_constant<int, 2>{}, raw[0]);
+            dma_chunk(2, 2);
+            load_chunk_a(3, std::integral_constant<int, 3>{}, raw[1]);
+            dma_chunk(3, 3);
+            wait_vmcnt<wide_bd_wait<-1, LOAD>()>();
         } else {
-            load_chunk(3, std::integral_constant<int, 3>{}, raw[1]);
+            load_chunk(0, std::integral_constant<int, 0>{}, raw[0]);
+            load_chunk(1, std::integral_constant<int, 1>{}, raw[1]);
+            build_table(0);
+            convert(raw[0], 0, 0);
+            convert(raw[1], 1, 1);
+            load_chunk(2, std::integral_constant<int, 2>{}, raw[0]);
+            if constexpr (RING == 4) {
+                convert(raw[0], 2, 2);
+                load_chunk(3, std::integral_constant<int, 3>{}, raw[1]);
+                load_chunk(4, std::integral_constant<int, 4>{}, raw[0]);
+            } else {
+                load_chunk(3, std::integral_constant<int, 3>{}, raw[1]);
+            }
         }
-        __syncthreads();
+        step_barrier();
 #pragma unroll
         for (int mi = 0; mi < MI; ++mi) load_frag_a(0, mi);
 #pragma unroll
@@ -317,12 +430,13 @@ gemm_wide_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
         }
         // the first steps convert into the slots after: every wave's reads of
         // chunk 0 must be complete first
-        __syncthreads();
+        step_barrier();
 
         // one chunk; J = the chunk's position in the 8-chunk iteration
         auto step = [&](int c0, auto jc) __attribute__((always_inline)) {
             constexpr int J = decltype(jc)::value;
             constexpr int st_next = (J + 1) % RING, st_conv = (J + LEAD) % RING;   // LDS slots
+            constexpr int sb_next = BD ? (J + 1) % C::RB : st_next;       // B slot of chunk c + 1
             constexpr int rset = (J + LEAD) & 1;                          // raw set of chunk c + LEAD
             const int c = c0 + J;
             // the block table for chunk c + LEAD when it starts a block
@@ -346,7 +460,7 @@ gemm_wide_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
                 // pin the FMAs here: otherwise they sink below the step's last
                 // MFMA with every product kept live
                 asm volatile("" : "+v"(acc[mi][ni]));
-                if (mi == MI - 1) load_scale(st_next, ni);
+                if (mi == MI - 1) load_scale(sb_next, ni);
             };
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
@@ -357,7 +471,7 @@ gemm_wide_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
                     fma_tile(t - 2);
                 }
                 if (ni == W_NI - 1) load_frag_a(st_next, mi);
-                if (mi == MI - 1) load_frag_b(st_next, ni);
+                if (mi == MI - 1) load_frag_b(sb_next, ni);
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
                     if (t != k * NT / 8 + 1) continue;
@@ -365,14 +479,19 @@ gemm_wide_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
                     // then take chunk c + LOAD's loads
                     convert_piece(raw[rset], k, (((J + LEAD) & 7) >> 2) == 0, st_conv);
                     if (k == 1) load_chunk_a(c + LOAD, std::integral_constant<int, (J + LOAD) & 7>{}, raw[rset]);
-                    if (k == 7) load_chunk_b(c + LOAD, raw[rset]);
+                    if constexpr (BD) {
+                        if (k == 4) dma_chunk(c + LOAD, J % C::RB);       // into chunk c's slot, read by now
+                    } else {
+                        if (k == 7) load_chunk_b(c + LOAD, raw[rset]);
+                    }
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
             fma_tile(NT - 2);
             fma_tile(NT - 1);
             __builtin_amdgcn_sched_barrier(0);
-            if (RING == 2 || (J & 1)) __syncthreads();
+            if constexpr (BD) wait_vmcnt<wide_bd_wait<J, LOAD>()>();        // chunk c + 2's B slot has landed
+            if (RING == 2 || (J & 1)) step_barrier();
         };
         for (int c0 = 0; c0 < nc; c0 += 8) {                            // nc % 8 == 0 (nb even)
             step(c0, std::integral_constant<int, 0>{});
@@ -384,6 +503,7 @@ gemm_wide_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
             step(c0, std::integral_constant<int, 6>{});
             step(c0, std::integral_constant<int, 7>{});
         }
+        if constexpr (BD) wait_vmcnt<0>();          // the DMAs past the last chunk have landed
     }
 
     // ---- store: lane holds rows 4g + i of each 16-row tile, token l16 --------
@@ -450,11 +570,41 @@ int gemm_wide_launch(const void * W, const void * Xq, float * Y, int64_t n_out, 
     const unsigned gy = (unsigned)((n_tok + WB_N - 1) / WB_N);
     const uint8_t * w = (const uint8_t *)W, * x = (const uint8_t *)Xq;
     if (mi == 5)
-        hipLaunchKernelGGL(gemm_wide_kernel<5>, dim3((unsigned)((n_out + 159) / 160), gy), dim3(512), 0, st, w, x, Y,
-                           (int)n_out, (int)n_tok, nb);
+        hipLaunchKernelGGL((gemm_wide_kernel<5, false>), dim3((unsigned)((n_out + 159) / 160), gy), dim3(512), 0, st,
+                           w, x, Y, (int)n_out, (int)n_tok, nb, nullptr, nullptr);
     else
-        hipLaunchKernelGGL(gemm_wide_kernel<8>, dim3((unsigned)((n_out + 255) / 256), gy), dim3(512), 0, st, w, x, Y,
-                           (int)n_out, (int)n_tok, nb);
+        hipLaunchKernelGGL((gemm_wide_kernel<8, false>), dim3((unsigned)((n_out + 255) / 256), gy), dim3(512), 0, st,
+                           w, x, Y, (int)n_out, (int)n_tok, nb, nullptr, nullptr);
+    return (int)hipGetLastError();
+}
+
+// Bytes of the activation in the layout the wide kernel DMAs (X16: f16 of
+// every q byte, 64 B per Q8_1 block; XD: its d as fp32), 0 if the 32-bit
+// buffer offsets cannot address it.
+int64_t gemm_wide_x16_bytes(int64_t n_tok, int nb) {
+    const int64_t blocks = n_tok * 4 * (int64_t)nb;
+    if (blocks * 64 >= (1ll << 31)) return 0;
+    return blocks * 68;
+}
+
+// The same product as gemm_wide_launch, with the activation converted once
+// into ws (gemm_wide_x16_bytes, 16-byte aligned) and the kernel's B side
+// arriving by LDS-DMA from there; bit-identical to gemm_wide_launch.
+int gemm_wide_launch_ws(const void * W, const void * Xq, float * Y, int64_t n_out, int64_t n_tok, int nb, int mi,
+                        void * ws, hipStream_t st) {
+    const int64_t blocks = n_tok * 4 * (int64_t)nb;
+    uint8_t * x16 = static_cast<uint8_t *>(ws);
+    float * xd = reinterpret_cast<float *>(x16 + blocks * 64);
+    hipLaunchKernelGGL(wide_x16_kernel, dim3((unsigned)((2 * blocks + 255) / 256)), dim3(256), 0, st,
+                       (const uint8_t *)Xq, x16, xd, blocks);
+    const unsigned gy = (unsigned)((n_tok + WB_N - 1) / WB_N);
+    const uint8_t * w = (const uint8_t *)W, * x = (const uint8_t *)Xq;
+    if (mi == 5)
+        hipLaunchKernelGGL((gemm_wide_kernel<5, true>), dim3((unsigned)((n_out + 159) / 160), gy), dim3(512), 0, st,
+                           w, x, Y, (int)n_out, (int)n_tok, nb, x16, xd);
+    else
+        hipLaunchKernelGGL((gemm_wide_kernel<8, true>), dim3((unsigned)((n_out + 255) / 256), gy), dim3(512), 0, st,
+                           w, x, Y, (int)n_out, (int)n_tok, nb, x16, xd);
     return (int)hipGetLastError();
 }
 

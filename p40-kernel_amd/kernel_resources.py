@@ -25,7 +25,7 @@ LLVM = "/opt/rocm/llvm/bin"
 # GEMMs, the FWHT / Q8_1 pre-passes, the repack and the PQ2_0 codec): a spill
 # or a scratch byte there is a regression.  The probes and the persistent
 # chain kernel are not on it.
-HOT_PATH = ("gemv_", "gemm_", "rot_quant", "quant_kernel", "swiglu_rot_quant", "rmsnorm_kernel",
+HOT_PATH = ("gemv_", "gemm_", "wide_x16", "rot_quant", "quant_kernel", "swiglu_rot_quant", "rmsnorm_kernel",
             "repack_kernel", "quantize_pq2_0", "dequantize_pq2_0")
 NOT_HOT = ("probe", "chain_kernel")
 

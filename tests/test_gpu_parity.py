@@ -905,6 +905,92 @@ def test_gemm_wide_kernel_edge_scales(mi, knobs):
     assert normwise(got["2"], O.gemm(W, Xq, n_out, n_in, n_tok, nthreads=16)) <= TOL
 
 
+def _gemm_pair(Wd, Xd, n_out, n_in, n_tok, dirty=True):
+    """Y from bonsai_p40_gemm and from bonsai_p40_gemm_ws (workspace filled
+    with 0xFF first, so that nothing stale can pass for converted data)."""
+    Y0 = torch.full((n_out, n_tok), float("nan"), dtype=torch.float32, device="cuda")
+    B.gemm(Wd, Xd, Y0, n_out, n_in, n_tok)
+    nws = B.gemm_workspace_bytes(n_in, n_tok)
+    ws = torch.full((max(nws, 16),), 255 if dirty else 0, dtype=torch.uint8, device="cuda")
+    Y1 = torch.full((n_out, n_tok), float("nan"), dtype=torch.float32, device="cuda")
+    B.gemm_ws(Wd, Xd, Y1, n_out, n_in, n_tok, ws)
+    return host(Y0), host(Y1)
+
+
+@pytest.mark.parametrize("mi", ["8", "5"])
+@pytest.mark.parametrize("n_out,n_in,n_tok", [(8200, 5120, 300), (8192, 1024, 77), (8193, 2048, 513),
+                                              (8211, 6144, 1000), (8192, 256, 17), (8192, 17408, 260)])
+def test_gemm_ws_wide_kernel(mi, n_out, n_in, n_tok, knobs):
+    """bonsai_p40_gemm_ws with the wide kernel forced on ragged shapes
+    (partial row and token tiles): the activation converted once into the
+    workspace and DMA'd into the tiles gives Y bit-identical to
+    bonsai_p40_gemm's staged conversion."""
+    case(f"gemm_ws wide kernel {n_out}x{n_in}x{n_tok} ({mi} x 32 rows)")
+    W = O.gen_weights(3700 + n_out, n_out, n_in)
+    X = np.stack([O.gen_normal(3701 + t, n_in) for t in range(n_tok)])
+    Xq = O.quantize_chunk_major(X)
+    knobs.set("BONSAI_GEMM_WIDE_MI", mi)
+    knobs.set("BONSAI_GEMM_WIDE", "2")
+    y0, y1 = _gemm_pair(dev(W), dev(Xq), n_out, n_in, n_tok)
+    assert np.all(np.isfinite(y1))
+    np.testing.assert_array_equal(bits(y1), bits(y0))
+    rows = np.r_[0:64, n_out - 64:n_out]
+    rb = n_in // 128 * 34
+    Ws = np.concatenate([W[r * rb:(r + 1) * rb] for r in rows])
+    assert normwise(y1[rows], O.gemm(Ws, Xq, rows.size, n_in, n_tok, nthreads=16)) <= TOL
+
+
+@pytest.mark.parametrize("mi", ["8", "5"])
+def test_gemm_ws_edge_scales(mi, knobs):
+    """The workspace path on subnormal, zero and |d| >= 32768 block scales
+    (the second pass over the big blocks restarts the activation DMA):
+    bit-identical to bonsai_p40_gemm."""
+    case(f"gemm_ws wide kernel 8200x2048x300 edge scales ({mi} x 32 rows)")
+    n_out, n_in, n_tok = 8200, 2048, 300
+    W = O.gen_weights(3500, n_out, n_in).copy()
+    nb = n_in // 128
+    rng = np.random.default_rng(36)
+    for r in range(n_out):
+        for b in rng.choice(nb, 3, replace=False):
+            off = (r * nb + b) * 34
+            if r % 3 == 0:
+                bits16 = np.uint16(rng.integers(0x7800, 0x7C00) | (0x8000 if rng.random() < 0.5 else 0))
+                W[off + 2:off + 34] = rng.integers(0, 256, 32, dtype=np.uint8)
+            else:
+                bits16 = np.uint16(rng.integers(0, 1024))
+            W[off:off + 2] = np.frombuffer(bits16.tobytes(), np.uint8)
+    X = O.gen_normal(3502, n_tok * n_in).reshape(n_tok, n_in)
+    Xq = O.quantize_chunk_major(X)
+    knobs.set("BONSAI_GEMM_WIDE_MI", mi)
+    knobs.set("BONSAI_GEMM_WIDE", "2")
+    y0, y1 = _gemm_pair(dev(W), dev(Xq), n_out, n_in, n_tok)
+    assert np.all(np.isfinite(y1))
+    np.testing.assert_array_equal(bits(y1), bits(y0))
+
+
+@pytest.mark.parametrize("n_out,n_in,n_tok", [(17408, 5120, 2048), (5120, 17408, 2048), (17408, 5120, 512),
+                                              (6144, 5120, 2048), (17408, 5120, 384), (4096, 5120, 16)])
+def test_gemm_ws_default_dispatch(n_out, n_in, n_tok):
+    """The default dispatch with a workspace on the prefill shapes (wide
+    tiles and the 128-row kernel for the rows they leave, one round of
+    160-row tiles, the LDS kernel alone at M = 384, the small-batch path at
+    16 tokens): bit-identical to bonsai_p40_gemm, called twice on one
+    workspace, and a NULL workspace runs bonsai_p40_gemm."""
+    case(f"gemm_ws default dispatch {n_out}x{n_in}x{n_tok}")
+    W = O.gen_weights(3800 + n_tok, n_out, n_in)
+    X = np.stack([O.fwht(O.gen_normal(3801 + t, n_in)) for t in range(n_tok)])
+    Xq = O.quantize_chunk_major(X)
+    Wd, Xd = dev(W), dev(Xq)
+    y0, y1 = _gemm_pair(Wd, Xd, n_out, n_in, n_tok)
+    assert np.all(np.isfinite(y1))
+    np.testing.assert_array_equal(bits(y1), bits(y0))
+    y0b, y1b = _gemm_pair(Wd, Xd, n_out, n_in, n_tok, dirty=False)
+    np.testing.assert_array_equal(bits(y1b), bits(y0))
+    Y2 = torch.full((n_out, n_tok), float("nan"), dtype=torch.float32, device="cuda")
+    B.gemm_ws(Wd, Xd, Y2, n_out, n_in, n_tok, None, 0)
+    np.testing.assert_array_equal(bits(host(Y2)), bits(y0))
+
+
 def test_gemm_equals_gemv_per_token():
     case("gemm n_tok=3 equals three gemv")
     n_out, n_in, n_tok = 300, 5120, 3

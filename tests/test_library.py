@@ -54,6 +54,8 @@ NULL = None
     ("bonsai_p40_gemm", (NULL, NULL, NULL, 16, 96, 4), 1),
     ("bonsai_p40_gemm", (NULL, NULL, NULL, 0, 128, 4), 0),
     ("bonsai_p40_gemm", (NULL, NULL, NULL, 16, 128, 0), 0),
+    ("bonsai_p40_gemm_ws", (NULL, NULL, NULL, 16, 96, 4, NULL, 0), 1),      # as bonsai_p40_gemm
+    ("bonsai_p40_gemm_ws", (NULL, NULL, NULL, 0, 128, 4, NULL, 0), 0),
     ("bonsai_p40_repack", (NULL, NULL, 4, 128 * 12), 1),        # nb % 8
     ("bonsai_p40_repack", (NULL, NULL, 0, 1024), 1),
     ("bonsai_p40_gemv_repack", (NULL, NULL, NULL, 4, 128 * 4), 1),
@@ -138,6 +140,7 @@ NULL_CASES = [
     ("bonsai_p40_rmsnorm_fwht_quant", (A, A, NULL, A, 1024, 1, EPS), (0, 1, 3)),
     ("bonsai_p40_swiglu_fwht_quant", (A, A, NULL, A, 1024), (0, 1, 3)),
     ("bonsai_p40_gemm", (A, A, A, 16, 128, 4), (0, 1, 2)),
+    ("bonsai_p40_gemm_ws", (A, A, A, 16, 128, 4, NULL, 0), (0, 1, 2)),
     ("bonsai_p40_repack", (A, A, 4, 1024), (0, 1)),
     ("bonsai_p40_gemv_repack", (A, A, A, 4, 1024), (0, 1, 2)),
     ("bonsai_p40_fwht", (A, NULL, 1024), (0,)),
@@ -187,6 +190,8 @@ LIMIT_CASES = [
     ("gemv: n_in / 128 > 2^24", "bonsai_p40_gemv", (A, A, A, 16, 128 * ((1 << 24) + 1))),
     ("gemv_repack: W not 8-byte aligned", "bonsai_p40_gemv_repack", (A + 4, A, A, 4, 1024)),
     ("gemm: W not 2-byte aligned", "bonsai_p40_gemm", (A + 1, A, A, 16, 128, 4)),
+    ("gemm_ws: workspace not 16-byte aligned", "bonsai_p40_gemm_ws", (A, A, A, 4096, 5120, 512, A + 4, 1 << 30)),
+    ("gemm_ws: workspace too small", "bonsai_p40_gemm_ws", (A, A, A, 4096, 5120, 512, A, 512 * 160 * 68 - 1)),
     ("fwht_quant: xq not 4-byte aligned", "bonsai_p40_fwht_quant", (A, NULL, A + 2, 1024)),
     ("quant_tokens: more than 65535 tokens", "bonsai_p40_quant_tokens", (A, NULL, A, 1024, 65536, 1)),
     ("quant_tokens: n * n_tok > 2^40", "bonsai_p40_quant_tokens", (A, NULL, A, 1 << 30, 2048, 0)),
@@ -291,3 +296,15 @@ def test_chain_plan_argument_checks():
     assert L.bonsai_p40_chain_run(None, 1, 256, None, None) == 1
     assert L.bonsai_p40_chain_run(256, 1, None, None, None) == 1
     assert L.bonsai_p40_chain_run(256, 0, 256, None, None) == 1
+
+
+def test_gemm_workspace_bytes():
+    """68 bytes per Q8_1 block of X (its q bytes as f16 and d as fp32); 0 for
+    an empty or invalid shape and where the converted activation would reach
+    2 GiB."""
+    L = B.lib()
+    assert B.gemm_workspace_bytes(5120, 2048) == 2048 * 160 * 68
+    assert B.gemm_workspace_bytes(17408, 512) == 512 * 544 * 68
+    assert L.bonsai_p40_gemm_workspace_bytes(5120, 0) == 0
+    assert L.bonsai_p40_gemm_workspace_bytes(100, 16) == 0
+    assert L.bonsai_p40_gemm_workspace_bytes(17408, 65536) == 0       # 65536 * 544 * 64 >= 2^31
