@@ -154,27 +154,46 @@ overlap_probe_kernel(int iters, int nf, uint32_t * __restrict__ sink) {
 __global__ void __launch_bounds__(256)
 gemm_core_probe_kernel(int iters, uint32_t * __restrict__ sink) {
     const int lane = threadIdx.x & 63;
-    v8h a, b;
+    // four distinct A operands (four equal MFMAs would be merged into one by
+    // the compiler) and a B operand that changes every iteration (so that no
+    // MFMA is loop-invariant): one f16 add per iteration beside the work
+    v8h a[4], b;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        a[i] = (_Float16)(0.001f * (float)(lane + i));
+#pragma unroll
+        for (int t = 0; t < 4; ++t) a[t][i] = (_Float16)(0.001f * (float)(lane + i + 7 * t));
         b[i] = (_Float16)(0.002f * (float)(lane - i));
     }
     float acc[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = 0.25f * (float)lane + (float)i;
     const float da = 1.0001f + 1e-6f * (float)lane;
-    for (int it = 0; it < iters; ++it) {
-        v4f s[4];
+    // software-pipelined as in the GEMM: the FMAs of iteration it fold the
+    // products of iteration it - 1, so the four products are live at once
+    // and no FMA waits for the MFMA just issued
+    // (two iterations per trip with the product sets alternating, so that no
+    // register copies carry them across)
+    v4f s0[4], s1[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) s0[t] = s1[t] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    auto step = [&](v4f (&out)[4], const v4f (&in)[4]) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-            s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            out[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], b, (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[4 * t + i] = fmaf(da, s[t][i], acc[4 * t + i]);
-        a[0] += (_Float16)1.0f;                     // a new A operand every iteration
+            for (int i = 0; i < 4; ++i) acc[4 * t + i] = fmaf(da, in[t][i], acc[4 * t + i]);
+        b[0] += (_Float16)1.0f;                     // a new B operand every iteration
+    };
+    for (int it = 0; it + 1 < iters; it += 2) {
+        step(s1, s0);
+        step(s0, s1);
     }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[4 * t + i] = fmaf(da, s0[t][i], acc[4 * t + i]);
     float z = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) z += acc[i];
