@@ -717,10 +717,17 @@ gemm_bd_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
         __builtin_amdgcn_wave_barrier();
         const uint8_t * wl = ring + slot * C::SLOT;
         // instruction m reads real activations only where column x's chunk is
-        // the chunk its K-group carries, zeros elsewhere
-        const uint8_t * bsrc[S::MPD];
+        // the chunk its K-group carries, zeros elsewhere.  The choice is a
+        // byte offset from the slot and the read is four dword loads: a
+        // 16-byte load at 4-byte alignment, or one through a choice between
+        // two pointers, reached the compiler without the alias information
+        // that tells it which LDS the load reads, and it then waited for every
+        // LDS-DMA in flight -- the next piece's included -- before the read,
+        // so no piece streamed beside the arithmetic of the one before it
+        const int zrel = (int)(zero - wl);
+        int bsrc[S::MPD];
 #pragma unroll
-        for (int m = 0; m < S::MPD; ++m) bsrc[m] = (col_ok && cc == 2 * m + gq) ? wl + b_off : zero;
+        for (int m = 0; m < S::MPD; ++m) bsrc[m] = (col_ok && cc == 2 * m + gq) ? b_off : zrel;
 #pragma unroll
         for (int bb = 0; bb < 2; ++bb) {
             float inner[RT][4];
@@ -735,7 +742,8 @@ gemm_bd_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
                 for (int mt = 0; mt < RT; ++mt) Dt[mt] = (v4ia){ns, ns, ns, ns};
 #pragma unroll
                 for (int m = 0; m < S::MPD; ++m) {
-                    const v4ia Bv = *reinterpret_cast<const v4ia4 *>(bsrc[m] + c0 * NT * Q81_BYTES);
+                    const int * bp = reinterpret_cast<const int *>(wl + bsrc[m] + c0 * NT * Q81_BYTES);
+                    const v4ia Bv = {bp[0], bp[1], bp[2], bp[3]};
 #pragma unroll
                     for (int mt = 0; mt < RT; ++mt) {
                         // code dword: chunk c0 + 2m + gq, half hh, row 16 mt + x (2-byte aligned in block 0)
@@ -849,7 +857,10 @@ int bd_choice(int nb, int64_t n_out, int64_t n_tok, int cus) {
     if (n_tok < 3 || n_tok > 8) return 0;
     const bool mfma4_width = nb == 8 || nb == 40 || nb == 48;
     if (mfma4_width && (n_tok == 4 || (n_tok == 3 && nb != 40))) return 0;
-    if (nb >= 96) return n_tok >= 5 ? 4 : 1;
+    // the 17408-column rows: 16 rows, K in 8 (µs, with the pieces streaming
+    // beside the arithmetic, 5120x17408, this choice / 32 rows, K in 8):
+    // B5 14.87 / 15.43, B6 15.24 / 15.58, B7 15.61 / 15.89, B8 16.20 / 16.31
+    if (nb >= 96) return 1;
     if (n_out >= 12288 && n_tok >= 6 && (n_out + 15) / 16 <= 8 * (int64_t)cus) return 5;
     if (n_out >= 12288 && n_tok >= 5) return n_tok >= 7 ? 3 : 2;
     return 1;
