@@ -530,7 +530,12 @@ gemm_small_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X
         const uint8_t * al = wl + C::W_BYTES;
 #pragma unroll
         for (int bb = 0; bb < 2; ++bb) {
-            float inner[RT][4];
+            // the block's four chunks: every MFMA first (four independent
+            // products in flight, their operand reads ahead of them), then
+            // the epilogues in chunk order -- one chunk at a time left each
+            // MFMA's latency and the LDS round trip before it exposed
+            v4ia S[4][RT];
+            float da[4];
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
                 // B: token column l16, K-group g of chunk 4bb + p; scale and -s of that token
@@ -539,7 +544,7 @@ gemm_small_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X
                 const uint32_t b0 = *reinterpret_cast<const uint32_t *>(ab + 4 + 8 * g);
                 const uint32_t b1 = *reinterpret_cast<const uint32_t *>(ab + 8 + 8 * g);
                 const int ns = -(int)(int16_t)(ds >> 16);
-                const float da = f16_bits_to_f32(ds & 0xffffu);
+                da[p] = f16_bits_to_f32(ds & 0xffffu);
                 const long Bv = __builtin_bit_cast(long, (v2i){(int)b0, (int)b1});
 #pragma unroll
                 for (int mt = 0; mt < RT; ++mt) {
@@ -556,19 +561,24 @@ gemm_small_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X
                     }
                     const long Av = __builtin_bit_cast(long, (v2i){(int)((w >> (2 * pr)) & 0x03030303u),
                                                                   (int)((w >> (2 * pr + 2)) & 0x03030303u)});
-                    const v4ia S = __builtin_amdgcn_mfma_i32_16x16x32_i8(Av, Bv, (v4ia){ns, ns, ns, ns}, 0, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        inner[mt][i] = p == 0 ? da * (float)S[i] : fmaf(da, (float)S[i], inner[mt][i]);
+                    S[p][mt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(Av, Bv, (v4ia){ns, ns, ns, ns}, 0, 0, 0);
                 }
-                // pin the chunk's epilogue here (otherwise every MFMA of the piece
-                // is hoisted into accumulator registers and converted at the end)
+            }
+            float inner[RT][4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
 #pragma unroll
                 for (int mt = 0; mt < RT; ++mt)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(inner[mt][i]));
-                __builtin_amdgcn_sched_barrier(0);
-            }
+                    for (int i = 0; i < 4; ++i)
+                        inner[mt][i] = p == 0 ? da[p] * (float)S[p][mt][i] : fmaf(da[p], (float)S[p][mt][i], inner[mt][i]);
+            // pin the block's epilogue here (otherwise the MFMAs of both blocks
+            // are hoisted together and converted at the end)
+#pragma unroll
+            for (int mt = 0; mt < RT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(inner[mt][i]));
+            __builtin_amdgcn_sched_barrier(0);
             // block scale of output rows 16 mt + 4g + i
 #pragma unroll
             for (int mt = 0; mt < RT; ++mt)
