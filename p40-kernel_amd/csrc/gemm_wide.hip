@@ -466,6 +466,11 @@ gemm_wide_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X,
             for (int t = 0; t < NT; ++t) {
                 const int mi = tile_mi(t), ni = tile_ni(t);
                 S[t & 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mi], Bf[ni], (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                // the MFMA issues before the epilogues that follow it: left
+                // free, the scheduler puts it after them, and each epilogue then
+                // reads a product only one MFMA old (hazard nops and a stall
+                // on the matrix core instead of two MFMAs of cover)
+                __builtin_amdgcn_sched_barrier(0);
                 if ((t & 1) && t >= 3) {
                     fma_tile(t - 3);
                     fma_tile(t - 2);
