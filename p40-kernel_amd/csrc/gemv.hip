@@ -843,14 +843,14 @@ gemv_nb_kernel(const MatGroup mg, const void * __restrict__ xin, const float * _
         float acc0[NT], acc1[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc0[t] = acc1[t] = 0.0f;
-        // the unit's LDS words.  Up to 5 slots (rows of up to 6144 columns,
-        // one token) every read is issued before any arithmetic, so the unit
-        // pays one LDS round trip: left to itself the compiler waited three
-        // times per unit (measured on MI355X, bit-identical, µs: 17408x5120
-        // 6.52-6.61 -> 6.45-6.51, gate+up grouped 11.45-11.79 -> 11.07-11.24;
-        // 17408-column rows, 9 slots, measured no better and keep the
-        // compiler's order)
-        constexpr bool HOIST = NT == 1 && !RP && P::S <= 5;
+        // the unit's LDS words.  Up to 5 slots (rows of up to 6144 columns)
+        // every read is issued before any arithmetic, so the unit pays one
+        // LDS round trip: left to itself the compiler waited three times per
+        // unit (measured on MI355X, bit-identical, µs: 17408x5120 6.52-6.61
+        // -> 6.45-6.51, gate+up grouped 11.45-11.79 -> 11.07-11.24, 2 tokens
+        // 9.57-9.62 -> 9.28-9.37; 17408-column rows, 9 slots, measured no
+        // better and keep the compiler's order)
+        constexpr bool HOIST = !RP && P::S <= 5;
         uint32_t cwr[HOIST ? P::S : 1][3], dwr[HOIST ? P::S : 1];
         if constexpr (HOIST) {
 #pragma unroll
