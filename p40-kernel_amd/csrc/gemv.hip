@@ -1351,6 +1351,27 @@ gemv_mfma4_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X
     float ykeep[NTG];
 #pragma unroll
     for (int g = 0; g < NTG; ++g) ykeep[g] = 0.0f;
+    // the lane's activation words (chunk 16 sl + b16 of its token) are the
+    // same in every unit: up to 10 slots they are read once and kept in
+    // registers (measured on MI355X, bit-identical, µs: 17408x5120 4 tokens
+    // 10.79-10.95 -> 10.24-10.35, 6144x5120 4 tokens 6.20-6.26 ->
+    // 6.14-6.19); the 12 slots of 6144-column rows measured slower so
+    // (5120x6144 6.54-6.59 -> 6.70-6.76) and read them per unit
+    constexpr bool KEEP = P::NS * NTG <= 10;
+    uint32_t awk[KEEP ? P::NS : 1][NTG][9];
+    if constexpr (KEEP) {
+#pragma unroll
+        for (int sl = 0; sl < P::NS; ++sl)
+#pragma unroll
+            for (int g = 0; g < NTG; ++g) {
+                const int t = 4 * g + i4;
+                const bool tv = t < n_tok;
+                const uint32_t * ab =
+                    reinterpret_cast<const uint32_t *>(&act_lds[Q81_BYTES * (tv ? (16 * sl + b16) * n_tok + t : 0)]);
+#pragma unroll
+                for (int k = 0; k < 9; ++k) awk[sl][g][k] = ab[k];
+            }
+    }
     for (int it = 0; it < nu; ++it) {
         const int slot = it & 1;
         wait_vmcnt<0>();
@@ -1380,10 +1401,15 @@ gemv_mfma4_kernel(const uint8_t * __restrict__ W, const uint8_t * __restrict__ X
                 const int t = 4 * g + i4;                      // this lane's token (column)
                 const bool tv = t < n_tok;
                 // unconditional reads (a missing token reads block 0 and is zeroed)
-                const uint32_t * ab = reinterpret_cast<const uint32_t *>(&act_lds[Q81_BYTES * (tv ? c * n_tok + t : 0)]);
-                uint32_t aw[9];
+                uint32_t awl[9];
+                const uint32_t * aw = awl;
+                if constexpr (KEEP) {
+                    aw = awk[sl][g];
+                } else {
+                    const uint32_t * ab = reinterpret_cast<const uint32_t *>(&act_lds[Q81_BYTES * (tv ? c * n_tok + t : 0)]);
 #pragma unroll
-                for (int k = 0; k < 9; ++k) aw[k] = ab[k];
+                    for (int k = 0; k < 9; ++k) awl[k] = ab[k];
+                }
                 const uint32_t ds = tv ? aw[0] : 0u;
                 const int ns = -(int)(int16_t)(ds >> 16);
                 v4i_t d = {ns, ns, ns, ns};
